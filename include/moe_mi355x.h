@@ -1,0 +1,210 @@
+/*
+ * moe_mi355x.h — C ABI of the MI355X (gfx950) Qwen3-MoE expert path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * (passed as void*, it is a hipStream_t; NULL means the legacy default
+ * stream).  All launches are asynchronous on that stream; no entry point
+ * synchronises, allocates device memory or reads device memory on the host.
+ * Outputs and workspaces are owned by the caller.
+ *
+ * Element types: "bf16" buffers hold IEEE bfloat16 as uint16; "f32" is IEEE
+ * float; indices are int64 where the reference exposes torch.long tensors and
+ * int32 for internal permutation maps.  Device pointers must be 16-byte
+ * aligned and row strides (in elements) multiples of 8.
+ *
+ * Return value: MOE_OK (0) or a negative MOE_ERR_* status; moe_last_error()
+ * gives a message for the last failure on the calling thread.
+ *
+ * Reference interfaces (paths relative to the reference checkout, "TF/" is the
+ * transformers package the reference pins, installed here as 5.15.0):
+ *   router     TF/models/qwen3_moe/modeling_qwen3_moe.py:249-267
+ *   experts    TF/integrations/moe.py:377-478 (grouped_mm_experts_forward)
+ *   aux loss   TF/models/qwen3_moe/modeling_qwen3_moe.py:514-593,
+ *              parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280
+ *   dispatch   parallel/parallel/engine/model_parallel/token_dispatch.py:78-174
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_ERR_INVALID (-1)     /* bad argument: null pointer, negative size, misalignment */
+#define MOE_ERR_UNSUPPORTED (-2) /* shape outside what the kernels handle */
+#define MOE_ERR_LAUNCH (-3)      /* hipLaunchKernel / HIP runtime failure */
+#define MOE_ERR_WORKSPACE (-4)   /* workspace smaller than *_workspace_bytes() */
+
+/* Message for the last non-zero status returned on this thread. */
+const char* moe_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int moe_abi_version(void);
+
+/* ------------------------------------------------------------------ router */
+
+/* logits[T,E] (f32) = x[T,H] (bf16) · wr[E,H]ᵀ (bf16), fp32 accumulation.
+ * Replaces F.linear in Qwen3MoeTopKRouter.forward
+ * (TF/models/qwen3_moe/modeling_qwen3_moe.py:260) computed as
+ * x.float() @ wr.float().T. */
+int moe_router_logits_fwd(const void* x, const void* wr, float* logits,
+                          int64_t T, int64_t H, int64_t E, void* stream);
+
+/* Per token: p = softmax(logits) in fp32; indices = the k largest, sorted
+ * descending (ties: lower expert index first); scores = p[indices],
+ * divided by their sum when norm_topk_prob != 0.
+ * Replaces softmax/topk/renorm of TF/models/qwen3_moe/modeling_qwen3_moe.py:261-265.
+ * 1 <= k <= min(E, 16), E <= 1024. */
+int moe_router_topk_fwd(const float* logits, float* scores, int64_t* indices,
+                        int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                        void* stream);
+
+/* Backward of moe_router_topk_fwd: d_logits[T,E] from d_scores[T,k].
+ * Writes (or, with accumulate != 0, adds into) f32 d_logits; also writes
+ * a bf16 copy of the result to d_logits_bf16 when it is not NULL.
+ * Autograd of TF/models/qwen3_moe/modeling_qwen3_moe.py:261-265. */
+int moe_router_topk_bwd(const float* logits, const int64_t* indices,
+                        const float* d_scores, int64_t T, int64_t E, int64_t k,
+                        int norm_topk_prob, float* d_logits, int accumulate,
+                        void* d_logits_bf16, void* stream);
+
+/* ---------------------------------------------------------------- aux loss */
+
+/* Switch load-balancing loss over logits[T,E] (f32):
+ *   p = softmax(logits); sel = topk(p, k);
+ *   W = sum_t w_t (w_t = token_weight[t], or 1 when token_weight is NULL);
+ *   c_e = sum_t w_t * #{j : sel[t,j] == e};  P_e = sum_t w_t * p[t,e];
+ *   aux = E * sum_e (c_e / W) * (P_e / W).
+ * Writes aux[0] and stats[E+1] = (c_0..c_{E-1}, W) for the backward.
+ * Replaces load_balancing_loss_func (TF/models/qwen3_moe/modeling_qwen3_moe.py:514-593)
+ * and, on one rank, sequence_parallel_load_balancing_loss
+ * (parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280).
+ * Deterministic (fixed-order reductions, no atomics). */
+size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E);
+int moe_aux_loss_fwd(const float* logits, const float* token_weight, int64_t T,
+                     int64_t E, int64_t k, float* aux, float* stats,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* d_logits[t,e] (+)= p_te * (g_te - sum_e' p_te' g_te'),
+ * g_te = d_aux[0] * E * w_t * c_e / W^2  (d_aux is a device scalar). */
+int moe_aux_loss_bwd(const float* logits, const float* token_weight,
+                     const float* stats, const float* d_aux, int64_t T,
+                     int64_t E, float* d_logits, int accumulate, void* stream);
+
+/* ----------------------------------------------------------------- permute */
+
+/* Stable counting sort of S = T*k routed slots by bucket = ids[s] / divisor
+ * (floor division; ids >= 0).  Slots whose bucket is >= num_buckets are
+ * sentinels: they sort after every real bucket and are excluded from counts.
+ * Outputs (int32):
+ *   perm[S]        sorted position -> slot index s = t*k + j
+ *   pos_of_slot[S] slot index -> sorted position (inverse of perm)
+ *   counts[nb]     slots per bucket (the send splits when bucket = owner rank)
+ *   offsets[nb]    inclusive cumsum of counts (offsets[nb-1] = valid rows)
+ * and, when permuted is not NULL, permuted[pos,:] = hidden[perm[pos]/k,:] for
+ * valid rows and zero for sentinel rows (bf16 rows of width H).
+ * Replaces torch.sort/gather/histc/cumsum of TF/integrations/moe.py:389-437
+ * (divisor 1, buckets = local experts, sentinel = num_experts) and the
+ * argsort/bincount/index_select of TokenDispatcher.dispatch,
+ * parallel/parallel/engine/model_parallel/token_dispatch.py:86-123
+ * (divisor = local expert count, buckets = EP ranks).
+ * num_buckets <= 1024. */
+size_t moe_permute_workspace_bytes(int64_t S, int64_t num_buckets);
+int moe_permute_fwd(const void* hidden, int64_t T, int64_t H,
+                    const int64_t* ids, int64_t k, int64_t divisor,
+                    int64_t num_buckets, void* permuted, int32_t* perm,
+                    int32_t* pos_of_slot, int32_t* counts, int32_t* offsets,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Per sorted position: local_ids[pos] = ids[perm[pos]] - bucket*divisor and
+ * routed_scores[pos] = scores[perm[pos]] (either output may be NULL).
+ * Replaces send_experts/send_scores of token_dispatch.py:124-125. */
+int moe_dispatch_meta(const int64_t* ids, const float* scores,
+                      const int32_t* perm, int64_t S, int64_t divisor,
+                      int64_t* local_ids, float* routed_scores, void* stream);
+
+/* Backward of the row gather: d_hidden[t,:] = sum_j d_permuted[pos_of_slot[t*k+j],:]
+ * over valid positions (pos < offsets[nb-1]), fp32 accumulation, plus
+ * d_add[t,:] when d_add is not NULL; bf16 in and out.
+ * Autograd of hidden_states[perm // k] (TF/integrations/moe.py:394) and of
+ * hidden_states.index_select (token_dispatch.py:123). */
+int moe_permute_bwd(const void* d_permuted, const int32_t* pos_of_slot,
+                    const int32_t* offsets, int64_t num_buckets, int64_t T,
+                    int64_t H, int64_t k, const void* d_add, void* d_hidden,
+                    void* stream);
+
+/* ----------------------------------------------------------------- combine */
+
+/* out[t,:] = sum_j s[t*k+j] * y[pos_of_slot[t*k+j],:] over valid positions,
+ * fp32 accumulation, bf16 out; s = 1 when scores is NULL.
+ * Replaces the weight/mask/inverse-permute/sum of TF/integrations/moe.py:461-478
+ * and, with scores NULL, the index_add of TokenDispatcher.combine
+ * (token_dispatch.py:169-174). */
+int moe_combine_fwd(const void* y, const int32_t* pos_of_slot,
+                    const int32_t* offsets, int64_t num_buckets,
+                    const float* scores, int64_t T, int64_t H, int64_t k,
+                    void* out, void* stream);
+
+/* Backward of moe_combine_fwd: d_y[pos,:] = s * d_out[t,:] (bf16) for valid
+ * positions, zero for sentinel rows; d_scores[t*k+j] = <y[pos,:], d_out[t,:]>
+ * (fp32, 0 for sentinels) when d_scores is not NULL. */
+int moe_combine_bwd(const void* d_out, const void* y,
+                    const int32_t* pos_of_slot, const int32_t* offsets,
+                    int64_t num_buckets, const float* scores, int64_t T,
+                    int64_t H, int64_t k, void* d_y, float* d_scores,
+                    void* stream);
+
+/* ------------------------------------------------------------ grouped GEMM */
+/* Groups partition the rows of the activation operand: group g owns rows
+ * [offs[g-1], offs[g]) (offs[-1] = 0; offs is the inclusive int32 cumsum,
+ * the F.grouped_mm `offs` convention of TF/integrations/moe.py:403).  Rows at
+ * or beyond offs[G-1] are not touched.  offs may be NULL for a single group
+ * of M rows (G must then be 1).  No host synchronisation: tiles are mapped to
+ * groups on the device. */
+
+/* act[M,I] = silu(gate) * up, pre[M,2I] = (gate | up), where
+ * (gate | up)[r,:] = xp[r,:] · w_gate_up[g]ᵀ, w_gate_up [G,2I,H] (first I rows
+ * are the gate).  Replaces F.grouped_mm up (TF/integrations/moe.py:440-442)
+ * plus _default_apply_gate (:509-521).  pre may be NULL. */
+int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up,
+                                const int32_t* offs, int64_t G, int64_t M,
+                                int64_t H, int64_t I, void* act, void* pre,
+                                void* stream);
+
+/* c[M,N] = a[M,K] · w[g]ᵀ with w [G,N,K].  Replaces F.grouped_mm down
+ * (TF/integrations/moe.py:456-459). */
+int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t* offs,
+                         int64_t G, int64_t M, int64_t N, int64_t K, void* c,
+                         void* stream);
+
+/* da[M,K] = dc[M,N] · w[g] with w [G,N,K] (input gradient of
+ * moe_grouped_gemm_fwd; autograd formula restated at TF/integrations/moe.py:236). */
+int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32_t* offs,
+                           int64_t G, int64_t M, int64_t N, int64_t K,
+                           void* da, void* stream);
+
+/* d_act[M,I] = dy[M,H] · w_down[g] (w_down [G,H,I]) fused with the SwiGLU
+ * backward against the saved pre[M,2I]: writes d_pre[M,2I] = (d_gate | d_up). */
+int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down,
+                                      const void* pre, const int32_t* offs,
+                                      int64_t G, int64_t M, int64_t H,
+                                      int64_t I, void* d_pre, void* stream);
+
+/* dw[g] [N,K] (+)= dc[rows of g, N]ᵀ · a[rows of g, K] (weight gradient of
+ * moe_grouped_gemm_fwd; TF/integrations/moe.py:237).  Empty groups get zeros
+ * (accumulate == 0) or are left untouched (accumulate != 0).
+ * dw_is_f32 selects an f32 instead of a bf16 dw buffer. */
+int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs,
+                           int64_t G, int64_t M, int64_t N, int64_t K,
+                           void* dw, int dw_is_f32, int accumulate,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

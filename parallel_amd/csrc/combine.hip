@@ -1,0 +1,177 @@
+// Weighted combine of expert rows back into token order, and its backward.
+//
+// Gather form, one 64-lane wave per token, 16 bytes (8 bf16) per lane per
+// step: the k expert rows of a token are read, scaled and summed in fp32 and
+// written once.  No atomics, so the result is deterministic; the backward
+// reads each token's output gradient once and produces both the row gradients
+// and the routing-score gradients (a wave dot product per routed slot).
+//
+// Reference: TF/integrations/moe.py:461-478 (weight, mask, inverse permute,
+// sum over k in fp32) and parallel/parallel/engine/model_parallel/
+// token_dispatch.py:160-174 (index_add combine, unweighted).
+#include "common.h"
+
+namespace moe {
+
+constexpr int kCombThreads = 256;
+constexpr int kCombWaves = kCombThreads / kWave;
+constexpr int kMaxK = 16;
+
+__device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
+  f[0] = lo_bf16(v.x); f[1] = hi_bf16(v.x);
+  f[2] = lo_bf16(v.y); f[3] = hi_bf16(v.y);
+  f[4] = lo_bf16(v.z); f[5] = hi_bf16(v.z);
+  f[6] = lo_bf16(v.w); f[7] = hi_bf16(v.w);
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  uint4 o;
+  o.x = pack_bf16x2(f[0], f[1]);
+  o.y = pack_bf16x2(f[2], f[3]);
+  o.z = pack_bf16x2(f[4], f[5]);
+  o.w = pack_bf16x2(f[6], f[7]);
+  return o;
+}
+
+__global__ __launch_bounds__(kCombThreads) void combine_fwd_kernel(const bf16_t* __restrict__ y,
+                                                                    const int32_t* __restrict__ pos_of_slot,
+                                                                    const int32_t* __restrict__ n_valid_ptr,
+                                                                    const float* __restrict__ scores, int T, int H,
+                                                                    int k, bf16_t* __restrict__ out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n_valid = *n_valid_ptr;
+  const int nchunk = H / 8;
+  for (int t = blockIdx.x * kCombWaves + (threadIdx.x >> 6); t < T; t += gridDim.x * kCombWaves) {
+    int pos[kMaxK];
+    float w[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      pos[j] = n_valid;
+      w[j] = 0.0f;
+      if (j < k) {
+        pos[j] = pos_of_slot[static_cast<int64_t>(t) * k + j];
+        w[j] = scores ? scores[static_cast<int64_t>(t) * k + j] : 1.0f;
+      }
+    }
+    for (int c = lane; c < nchunk; c += kWave) {
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j) {
+        if (j < k && pos[j] < n_valid) {
+          float f[8];
+          unpack8(reinterpret_cast<const uint4*>(y + static_cast<int64_t>(pos[j]) * H)[c], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += f[e] * w[j];
+        }
+      }
+      reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * H)[c] = pack8(acc);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kCombThreads) void combine_bwd_kernel(const bf16_t* __restrict__ d_out,
+                                                                    const bf16_t* __restrict__ y,
+                                                                    const int32_t* __restrict__ pos_of_slot,
+                                                                    const int32_t* __restrict__ n_valid_ptr,
+                                                                    const float* __restrict__ scores, int T, int H,
+                                                                    int k, bf16_t* __restrict__ d_y,
+                                                                    float* __restrict__ d_scores) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n_valid = *n_valid_ptr;
+  const int nchunk = H / 8;
+  for (int t = blockIdx.x * kCombWaves + (threadIdx.x >> 6); t < T; t += gridDim.x * kCombWaves) {
+    int pos[kMaxK];
+    float w[kMaxK], dot[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      pos[j] = n_valid;
+      w[j] = 0.0f;
+      dot[j] = 0.0f;
+      if (j < k) {
+        pos[j] = pos_of_slot[static_cast<int64_t>(t) * k + j];
+        w[j] = scores ? scores[static_cast<int64_t>(t) * k + j] : 1.0f;
+      }
+    }
+    for (int c = lane; c < nchunk; c += kWave) {
+      float g[8];
+      unpack8(reinterpret_cast<const uint4*>(d_out + static_cast<int64_t>(t) * H)[c], g);
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j) {
+        if (j < k) {
+          uint4* dst = reinterpret_cast<uint4*>(d_y + static_cast<int64_t>(pos[j]) * H) + c;
+          if (pos[j] < n_valid) {
+            if (d_scores) {
+              float f[8];
+              unpack8(reinterpret_cast<const uint4*>(y + static_cast<int64_t>(pos[j]) * H)[c], f);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) dot[j] += f[e] * g[e];
+            }
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = g[e] * w[j];
+            *dst = pack8(o);
+          } else {
+            *dst = make_uint4(0, 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (d_scores) {
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j) {
+        if (j < k) {
+          float s = wave_sum(dot[j]);
+          if (lane == 0) d_scores[static_cast<int64_t>(t) * k + j] = s;
+        }
+      }
+    }
+  }
+}
+
+int token_grid(int64_t T) {
+  int64_t b = (T + kCombWaves - 1) / kCombWaves;
+  if (b > 8192) b = 8192;
+  return static_cast<int>(b < 1 ? 1 : b);
+}
+
+int check_combine(const void* rows, const int32_t* pos_of_slot, const int32_t* offsets, int64_t nb, int64_t T,
+                  int64_t H, int64_t k, const void* out) {
+  MOE_REQUIRE(T >= 0 && T < (1ll << 31) && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0, MOE_ERR_INVALID,
+              "combine: bad sizes T=%lld H=%lld k=%lld (H %% 8 == 0, 1 <= k <= %d)", (long long)T, (long long)H,
+              (long long)k, kMaxK);
+  MOE_REQUIRE(nb >= 1, MOE_ERR_INVALID, "combine: num_buckets must be >= 1");
+  if (T == 0) return MOE_OK;
+  MOE_REQUIRE(rows && pos_of_slot && offsets && out, MOE_ERR_INVALID, "combine: null pointer");
+  MOE_REQUIRE(aligned16(rows) && aligned16(out), MOE_ERR_INVALID, "combine: buffers must be 16-byte aligned");
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_combine_fwd(const void* y, const int32_t* pos_of_slot, const int32_t* offsets,
+                               int64_t num_buckets, const float* scores, int64_t T, int64_t H, int64_t k, void* out,
+                               void* stream) {
+  int rc = check_combine(y, pos_of_slot, offsets, num_buckets, T, H, k, out);
+  if (rc || T == 0) return rc;
+  hipLaunchKernelGGL(combine_fwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
+                     static_cast<const bf16_t*>(y), pos_of_slot, offsets + (num_buckets - 1), scores,
+                     static_cast<int>(T), static_cast<int>(H), static_cast<int>(k), static_cast<bf16_t*>(out));
+  return launch_status("moe_combine_fwd");
+}
+
+extern "C" int moe_combine_bwd(const void* d_out, const void* y, const int32_t* pos_of_slot, const int32_t* offsets,
+                               int64_t num_buckets, const float* scores, int64_t T, int64_t H, int64_t k, void* d_y,
+                               float* d_scores, void* stream) {
+  int rc = check_combine(d_out, pos_of_slot, offsets, num_buckets, T, H, k, d_y);
+  if (rc || T == 0) return rc;
+  MOE_REQUIRE(!d_scores || (y && aligned16(y)), MOE_ERR_INVALID, "combine bwd: d_scores needs y");
+  hipLaunchKernelGGL(combine_bwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
+                     static_cast<const bf16_t*>(d_out), static_cast<const bf16_t*>(y), pos_of_slot,
+                     offsets + (num_buckets - 1), scores, static_cast<int>(T), static_cast<int>(H),
+                     static_cast<int>(k), static_cast<bf16_t*>(d_y), d_scores);
+  return launch_status("moe_combine_bwd");
+}

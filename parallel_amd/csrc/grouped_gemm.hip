@@ -1,0 +1,697 @@
+// Grouped bf16 GEMMs for the MoE expert path on gfx950 (MI355X).
+//
+// One kernel template covers the three contraction shapes of an expert layer:
+//   MG / B K-contiguous   forward      c[r,n]   = sum_k a[r,k] w[g][n,k]
+//   MG / B N-contiguous   input grad   da[r,n]  = sum_k dc[r,k] w[g][k,n]
+//   KG                    weight grad  dw[g][m,n] = sum_{r in g} dc[r,m] a[r,n]
+// MG = groups partition the rows of the activation operand (variable M per
+// expert), KG = groups partition the reduction (variable K per expert).
+//
+// Tiling: 256 threads = 4 waves in a 2x2 grid; each wave owns a
+// (BM/2)x(BN/2) block of 32x32 MFMA sub-tiles (v_mfma_f32_32x32x16_bf16).
+// Operands are staged through LDS as K-contiguous rows (row stride BK+8 to
+// spread banks) with double buffering and register prefetch of the next
+// k-tile.  Operands that are contiguous along M/N in HBM are transposed in
+// registers (4x8 bf16 blocks, v_perm) on their way into LDS so every MFMA
+// fragment read is one 16-byte ds_read.
+//
+// Tiles are mapped to groups on the device from the `offs` cumsum (no host
+// sync).  The logical tile order is group-major, then n-tile, then m-tile, so
+// consecutive tiles share an expert's weight tile and its activation rows;
+// the launch index is remapped so that each XCD (blocks are dealt round-robin
+// over the 8 XCDs) gets a contiguous run of logical tiles and the sharing
+// happens in that XCD's L2.
+#include <stdarg.h>
+
+#include "common.h"
+
+namespace moe {
+
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU_FWD = 2, EPI_SWIGLU_BWD = 3, EPI_WGRAD = 4 };
+enum { MODE_MG = 0, MODE_KG = 1 };
+
+constexpr int kThreads = 256;
+constexpr int kNumXcd = 8;
+
+struct GemmParams {
+  const bf16_t* A;  // MG: [rows, K] (lda);  KG: [rows, M] (lda)
+  const bf16_t* B;  // MG: per group (stride_bg) [N, K] or [K, N] (ldb);  KG: [rows, N] (ldb)
+  void* C;          // MG: [rows, ldc];  KG: per group (stride_cg) [M, N] (ldc)
+  void* C2;         // SWIGLU_FWD: pre-activation [rows, 2N] (may be null)
+  const bf16_t* P;  // SWIGLU_BWD: saved pre-activation [rows, 2N]
+  const int32_t* offs;
+  int G;
+  int rows;  // total activation rows (M for MG; sum of K for KG)
+  int M, N, K;  // GEMM-internal sizes: MG: M = rows, N out cols, K reduction; KG: M x N output per group
+  int64_t lda, ldb, ldc, ldp;
+  int64_t stride_bg, stride_cg;
+  int swiglu_I;  // SWIGLU_FWD: intermediate size I (weight rows gate: [0,I), up: [I,2I))
+  int accumulate;
+  int n_tiles, m_tiles_max, total_blocks;
+};
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ uint32_t sel_lo(uint32_t a, uint32_t b) {
+  // low halves: (lo16(a), lo16(b)) packed as a | b<<16
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t sel_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// Column c (0..7) of a 4x8 bf16 block given as four 16-byte rows, returned as
+// 4 bf16 (k = 0..3) in two dwords.
+__device__ __forceinline__ uint2 column4(const uint4 (&v)[4], int c) {
+  uint32_t w0, w1, w2, w3;
+  switch (c >> 1) {
+    case 0: w0 = v[0].x; w1 = v[1].x; w2 = v[2].x; w3 = v[3].x; break;
+    case 1: w0 = v[0].y; w1 = v[1].y; w2 = v[2].y; w3 = v[3].y; break;
+    case 2: w0 = v[0].z; w1 = v[1].z; w2 = v[2].z; w3 = v[3].z; break;
+    default: w0 = v[0].w; w1 = v[1].w; w2 = v[2].w; w3 = v[3].w; break;
+  }
+  uint2 r;
+  if (c & 1) {
+    r.x = sel_hi(w0, w1);
+    r.y = sel_hi(w2, w3);
+  } else {
+    r.x = sel_lo(w0, w1);
+    r.y = sel_lo(w2, w3);
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint4 ldg16(const bf16_t* p, bool valid) {
+  uint4 z = make_uint4(0, 0, 0, 0);
+  return valid ? *reinterpret_cast<const uint4*>(p) : z;
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+
+// Find the group g whose tile range holds logical tile L, given per-group tile
+// counts ntile(g) = n_mult * ceil(cnt_g / BM).  Every wave of the block runs
+// this redundantly (no LDS, no barrier).  Returns false if L is past the end.
+template <int BM>
+__device__ __forceinline__ bool locate_group(const int32_t* offs, int G, int rows, int n_mult, int L, int& g_out,
+                                             int& tile0_out, int& row0_out, int& cnt_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int base = 0;  // tiles before this chunk
+  for (int c0 = 0; c0 < G; c0 += kWave) {
+    int g = c0 + lane;
+    int lo = 0, hi = 0;
+    if (g < G) {
+      // Clamped so that malformed offsets can never address rows outside [0, rows).
+      hi = min(max(offs[g], 0), rows);
+      lo = g ? min(max(offs[g - 1], 0), hi) : 0;
+    }
+    int cnt = hi - lo;
+    int nt = n_mult * ((cnt + BM - 1) / BM);
+    int incl = wave_inclusive_scan(nt);
+    unsigned long long hit = __ballot(g < G && L < base + incl);
+    if (hit) {
+      int src = __ffsll(hit) - 1;
+      int excl = incl - nt;
+      g_out = c0 + src;
+      tile0_out = base + __shfl(excl, src, kWave);
+      row0_out = __shfl(lo, src, kWave);
+      cnt_out = __shfl(cnt, src, kWave);
+      return true;
+    }
+    base += __shfl(incl, kWave - 1, kWave);
+  }
+  return false;
+}
+
+// ------------------------------------------------------------------ kernel
+
+template <int MODE, bool B_KCONTIG, int EPI, int BM, int BN, int BK>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams p) {
+  constexpr int LDS_STRIDE = BK + 8;  // elements
+  constexpr int SM = BM / 64;         // 32x32 sub-tiles per wave along M
+  constexpr int SN = BN / 64;         // ... along N
+  constexpr int A_KCONTIG = (MODE == MODE_MG);
+  constexpr bool BK_CONTIG = (MODE == MODE_MG) && B_KCONTIG;
+  static_assert(BK % 16 == 0, "BK must be a multiple of the MFMA K (16)");
+  static_assert((BM * BK) % (8 * kThreads) == 0 && (BN * BK) % (8 * kThreads) == 0, "tile too small for loader");
+  static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
+
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LDS_STRIDE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // XCD-aware remap of the launch index to a logical tile index.
+  const int nb = p.total_blocks;  // multiple of kNumXcd
+  const int bid = blockIdx.x;
+  const int L = (bid % kNumXcd) * (nb / kNumXcd) + bid / kNumXcd;
+
+  // ------------------------------------------------------ tile -> work
+  int g, m0, n0;             // group, first output row (within group for KG), first output col
+  int row_begin, row_end;    // MG: absolute activation rows of the group; KG: reduction rows
+  const bf16_t* Bg = p.B;
+  if constexpr (MODE == MODE_MG) {
+    if (p.offs) {
+      int tile0, row0, cnt;
+      if (!locate_group<BM>(p.offs, p.G, p.rows, p.n_tiles, L, g, tile0, row0, cnt)) return;
+      int local = L - tile0;
+      int mt_g = (cnt + BM - 1) / BM;
+      int nt = local / mt_g;
+      int mt = local - nt * mt_g;
+      row_begin = row0;
+      row_end = row0 + cnt;
+      m0 = row0 + mt * BM;  // absolute row
+      n0 = nt * BN;
+    } else {
+      int mtiles = (p.M + BM - 1) / BM;
+      if (L >= mtiles * p.n_tiles) return;
+      g = 0;
+      int nt = L / mtiles;
+      int mt = L - nt * mtiles;
+      row_begin = 0;
+      row_end = p.M;
+      m0 = mt * BM;
+      n0 = nt * BN;
+    }
+    Bg = p.B + static_cast<int64_t>(g) * p.stride_bg;
+  } else {
+    const int per_group = p.n_tiles * p.m_tiles_max;
+    g = L / per_group;
+    if (g >= p.G) return;
+    int local = L - g * per_group;
+    int nt = local / p.m_tiles_max;
+    int mt = local - nt * p.m_tiles_max;
+    row_end = p.offs ? min(max(p.offs[g], 0), p.rows) : p.rows;
+    row_begin = p.offs ? (g ? min(max(p.offs[g - 1], 0), row_end) : 0) : 0;
+    m0 = mt * BM;
+    n0 = nt * BN;
+  }
+
+  // Reduction length for this tile.
+  const int Kred = (MODE == MODE_MG) ? p.K : (row_end - row_begin);
+
+  f32x16_t acc[SM][SN];
+#pragma unroll
+  for (int i = 0; i < SM; ++i)
+#pragma unroll
+    for (int j = 0; j < SN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if constexpr (MODE == MODE_KG) {
+    if (Kred <= 0) {
+      // Empty group: the weight gradient is zero.
+      if (p.accumulate) return;
+    }
+  }
+
+  // ------------------------------------------------------ loaders
+  // K-contiguous operand: R rows x BK, 16-byte chunks.
+  constexpr int CH = BK / 8;
+  constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (BM * BK / 32) / kThreads;
+  constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (BN * BK / 32) / kThreads;
+
+  // Per-thread row pointers for K-contiguous operands (fixed over k).
+  const bf16_t* a_row_ptr[A_KCONTIG ? NLA : 1];
+  bool a_row_ok[A_KCONTIG ? NLA : 1];
+  const bf16_t* b_row_ptr[BK_CONTIG ? NLB : 1];
+  bool b_row_ok[BK_CONTIG ? NLB : 1];
+
+  if constexpr (A_KCONTIG) {
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      int c = tid + i * kThreads;
+      int r = c / CH;
+      int grow = m0 + r;
+      a_row_ok[i] = grow < row_end;
+      a_row_ptr[i] = p.A + static_cast<int64_t>(a_row_ok[i] ? grow : row_begin) * p.lda;
+    }
+  }
+  if constexpr (BK_CONTIG) {
+#pragma unroll
+    for (int i = 0; i < NLB; ++i) {
+      int c = tid + i * kThreads;
+      int r = c / CH;
+      int wrow;
+      bool ok;
+      if constexpr (EPI == EPI_SWIGLU_FWD) {
+        // Tile row r -> (wave column, sub-tile, half): first SN/2 sub-tiles of
+        // each wave column are gate rows, the rest the matching up rows.
+        int wcol = r / (BN / 2);
+        int within = r % (BN / 2);
+        int sn = within / 32;
+        int half = sn / (SN / 2);
+        int act_col = (n0 / 2) + wcol * (BN / 4) + (sn % (SN / 2)) * 32 + (within % 32);
+        ok = act_col < p.swiglu_I;
+        wrow = half * p.swiglu_I + act_col;
+      } else {
+        wrow = n0 + r;
+        ok = wrow < p.N;
+      }
+      b_row_ok[i] = ok;
+      b_row_ptr[i] = Bg + static_cast<int64_t>(ok ? wrow : 0) * p.ldb;
+    }
+  }
+
+  uint4 ra[A_KCONTIG ? NLA : NLA * 4];
+  uint4 rb[BK_CONTIG ? NLB : NLB * 4];
+
+  auto load_tile = [&](int k0) {
+    // A
+    if constexpr (A_KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < NLA; ++i) {
+        int c = tid + i * kThreads;
+        int kc = (c % CH) * 8;
+        ra[i] = ldg16(a_row_ptr[i] + k0 + kc, a_row_ok[i] && (k0 + kc) < Kred);
+      }
+    } else {
+      // A is M-contiguous: tile = BK reduction rows x BM columns, 4x8 blocks.
+      constexpr int NBM = BM / 8;
+#pragma unroll
+      for (int i = 0; i < NLA; ++i) {
+        int blk = tid + i * kThreads;
+        int mb = blk % NBM, kb = blk / NBM;
+        int col = m0 + mb * 8;
+        bool col_ok = col < p.M;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int kk = k0 + kb * 4 + q;
+          bool ok = col_ok && kk < Kred;
+          ra[i * 4 + q] = ldg16(p.A + static_cast<int64_t>(row_begin + (ok ? kk : 0)) * p.lda + (ok ? col : 0), ok);
+        }
+      }
+    }
+    // B
+    if constexpr (BK_CONTIG) {
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        int c = tid + i * kThreads;
+        int kc = (c % CH) * 8;
+        rb[i] = ldg16(b_row_ptr[i] + k0 + kc, b_row_ok[i] && (k0 + kc) < Kred);
+      }
+    } else {
+      constexpr int NBN = BN / 8;
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        int blk = tid + i * kThreads;
+        int nbk = blk % NBN, kb = blk / NBN;
+        int col = n0 + nbk * 8;
+        bool col_ok = col < p.N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int kk = k0 + kb * 4 + q;
+          bool ok = col_ok && kk < Kred;
+          int64_t rowi = (MODE == MODE_KG) ? static_cast<int64_t>(row_begin + (ok ? kk : 0)) : (ok ? kk : 0);
+          rb[i * 4 + q] = ldg16(Bg + rowi * p.ldb + (ok ? col : 0), ok);
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    bf16_t* as = As[buf];
+    bf16_t* bs = Bs[buf];
+    if constexpr (A_KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < NLA; ++i) {
+        int c = tid + i * kThreads;
+        int r = c / CH, kc = (c % CH) * 8;
+        *reinterpret_cast<uint4*>(as + r * LDS_STRIDE + kc) = ra[i];
+      }
+    } else {
+      constexpr int NBM = BM / 8;
+#pragma unroll
+      for (int i = 0; i < NLA; ++i) {
+        int blk = tid + i * kThreads;
+        int mb = blk % NBM, kb = blk / NBM;
+        uint4 v[4] = {ra[i * 4 + 0], ra[i * 4 + 1], ra[i * 4 + 2], ra[i * 4 + 3]};
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          *reinterpret_cast<uint2*>(as + (mb * 8 + c) * LDS_STRIDE + kb * 4) = column4(v, c);
+      }
+    }
+    if constexpr (BK_CONTIG) {
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        int c = tid + i * kThreads;
+        int r = c / CH, kc = (c % CH) * 8;
+        *reinterpret_cast<uint4*>(bs + r * LDS_STRIDE + kc) = rb[i];
+      }
+    } else {
+      constexpr int NBN = BN / 8;
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        int blk = tid + i * kThreads;
+        int nbk = blk % NBN, kb = blk / NBN;
+        uint4 v[4] = {rb[i * 4 + 0], rb[i * 4 + 1], rb[i * 4 + 2], rb[i * 4 + 3]};
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          *reinterpret_cast<uint2*>(bs + (nbk * 8 + c) * LDS_STRIDE + kb * 4) = column4(v, c);
+      }
+    }
+  };
+
+  const int frag_row = lane & 31;
+  const int frag_k = (lane >> 5) * 8;
+
+  auto compute_tile = [&](int buf) {
+    const bf16_t* as = As[buf] + (wm * (BM / 2) + frag_row) * LDS_STRIDE + frag_k;
+    const bf16_t* bs = Bs[buf] + (wn * (BN / 2) + frag_row) * LDS_STRIDE + frag_k;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t af[SM], bfr[SN];
+#pragma unroll
+      for (int i = 0; i < SM; ++i) af[i] = *reinterpret_cast<const bf16x8_t*>(as + i * 32 * LDS_STRIDE + ks * 16);
+#pragma unroll
+      for (int j = 0; j < SN; ++j) bfr[j] = *reinterpret_cast<const bf16x8_t*>(bs + j * 32 * LDS_STRIDE + ks * 16);
+#pragma unroll
+      for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+          // Operands swapped: the result holds C^T fragments, so each lane
+          // owns one output row and runs of 4 consecutive output columns.
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = (Kred + BK - 1) / BK;
+  if (nk > 0) {
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_tile((kt + 1) * BK);
+      compute_tile(cur);
+      if (kt + 1 < nk) store_tile(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ------------------------------------------------------ epilogue
+  // Lane owns output row  wm*(BM/2) + i*32 + (lane & 31)  and columns
+  // wn*(BN/2) + j*32 + 8*q + 4*(lane >> 5) + {0..3} holding acc[i][j][4q..4q+3].
+  const int col_lane = 4 * (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < SM; ++i) {
+    const int row = m0 + wm * (BM / 2) + i * 32 + (lane & 31);
+    bool row_ok;
+    if constexpr (MODE == MODE_MG) row_ok = row < row_end;
+    else row_ok = row < p.M;
+    if (!row_ok) continue;
+    if constexpr (EPI == EPI_SWIGLU_FWD) {
+#pragma unroll
+      for (int j = 0; j < SN / 2; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = (n0 / 2) + wn * (BN / 4) + j * 32 + 8 * q + col_lane;
+          if (col >= p.swiglu_I) continue;
+          float gt[4], up[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            gt[e] = acc[i][j][4 * q + e];
+            up[e] = acc[i][j + SN / 2][4 * q + e];
+          }
+          uint2 act;
+          act.x = pack_bf16x2(silu_f(gt[0]) * up[0], silu_f(gt[1]) * up[1]);
+          act.y = pack_bf16x2(silu_f(gt[2]) * up[2], silu_f(gt[3]) * up[3]);
+          *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = act;
+          if (p.C2) {
+            bf16_t* pre = static_cast<bf16_t*>(p.C2) + static_cast<int64_t>(row) * p.ldp;
+            uint2 gv, uv;
+            gv.x = pack_bf16x2(gt[0], gt[1]);
+            gv.y = pack_bf16x2(gt[2], gt[3]);
+            uv.x = pack_bf16x2(up[0], up[1]);
+            uv.y = pack_bf16x2(up[2], up[3]);
+            *reinterpret_cast<uint2*>(pre + col) = gv;
+            *reinterpret_cast<uint2*>(pre + p.swiglu_I + col) = uv;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < SN; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = n0 + wn * (BN / 2) + j * 32 + 8 * q + col_lane;
+          if (col >= p.N) continue;
+          float v0 = acc[i][j][4 * q + 0], v1 = acc[i][j][4 * q + 1];
+          float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+          if constexpr (EPI == EPI_BF16) {
+            uint2 o;
+            o.x = pack_bf16x2(v0, v1);
+            o.y = pack_bf16x2(v2, v3);
+            *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = o;
+          } else if constexpr (EPI == EPI_F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) =
+                make_float4(v0, v1, v2, v3);
+          } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+            // v = d_act at (row, col..col+3); pre holds (gate | up).
+            const bf16_t* pre = p.P + static_cast<int64_t>(row) * p.ldp;
+            uint2 gw = *reinterpret_cast<const uint2*>(pre + col);
+            uint2 uw = *reinterpret_cast<const uint2*>(pre + p.N + col);
+            float gt[4] = {lo_bf16(gw.x), hi_bf16(gw.x), lo_bf16(gw.y), hi_bf16(gw.y)};
+            float up[4] = {lo_bf16(uw.x), hi_bf16(uw.x), lo_bf16(uw.y), hi_bf16(uw.y)};
+            float da[4] = {v0, v1, v2, v3};
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float s = 1.0f / (1.0f + __expf(-gt[e]));
+              float silu = gt[e] * s;
+              du[e] = da[e] * silu;
+              dg[e] = da[e] * up[e] * s * (1.0f + gt[e] * (1.0f - s));
+            }
+            bf16_t* out = static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc;
+            uint2 og, ou;
+            og.x = pack_bf16x2(dg[0], dg[1]);
+            og.y = pack_bf16x2(dg[2], dg[3]);
+            ou.x = pack_bf16x2(du[0], du[1]);
+            ou.y = pack_bf16x2(du[2], du[3]);
+            *reinterpret_cast<uint2*>(out + col) = og;
+            *reinterpret_cast<uint2*>(out + p.N + col) = ou;
+          } else {  // EPI_WGRAD: bf16 or f32 destination chosen by ldp (0 = bf16, 1 = f32)
+            int64_t off = static_cast<int64_t>(g) * p.stride_cg + static_cast<int64_t>(row) * p.ldc + col;
+            if (p.ldp) {
+              float4* dst = reinterpret_cast<float4*>(static_cast<float*>(p.C) + off);
+              if (p.accumulate) {
+                float4 o = *dst;
+                v0 += o.x; v1 += o.y; v2 += o.z; v3 += o.w;
+              }
+              *dst = make_float4(v0, v1, v2, v3);
+            } else {
+              uint2* dst = reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + off);
+              if (p.accumulate) {
+                uint2 o = *dst;
+                v0 += lo_bf16(o.x); v1 += hi_bf16(o.x); v2 += lo_bf16(o.y); v3 += hi_bf16(o.y);
+              }
+              uint2 ob;
+              ob.x = pack_bf16x2(v0, v1);
+              ob.y = pack_bf16x2(v2, v3);
+              *dst = ob;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ host side
+
+namespace {
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+template <int MODE, bool B_KCONTIG, int EPI>
+int launch(GemmParams& p, hipStream_t stream, const char* name) {
+  int blocks;
+  if (MODE == MODE_MG) {
+    p.m_tiles_max = (p.M + kBM - 1) / kBM + (p.offs ? p.G : 0);
+    blocks = p.m_tiles_max * p.n_tiles;
+  } else {
+    p.m_tiles_max = (p.M + kBM - 1) / kBM;
+    blocks = p.G * p.m_tiles_max * p.n_tiles;
+  }
+  if (blocks <= 0) return MOE_OK;
+  blocks = round_up(blocks, kNumXcd);
+  p.total_blocks = blocks;
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, B_KCONTIG, EPI, kBM, kBN, kBK>), dim3(blocks), dim3(kThreads), 0,
+                     stream, p);
+  return launch_status(name);
+}
+
+int check_common(const void* a, const void* b, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K) {
+  MOE_REQUIRE(a && b, MOE_ERR_INVALID, "grouped gemm: null operand");
+  MOE_REQUIRE(G >= 1 && G <= 4096, MOE_ERR_UNSUPPORTED, "grouped gemm: G=%lld outside [1,4096]", (long long)G);
+  MOE_REQUIRE(offs || G == 1, MOE_ERR_INVALID, "grouped gemm: offs may be NULL only for G == 1");
+  MOE_REQUIRE(M >= 0 && N > 0 && K > 0, MOE_ERR_INVALID, "grouped gemm: bad sizes M=%lld N=%lld K=%lld",
+              (long long)M, (long long)N, (long long)K);
+  MOE_REQUIRE(M < (1ll << 31) && N < (1 << 30) && K < (1 << 30), MOE_ERR_UNSUPPORTED, "grouped gemm: size overflow");
+  MOE_REQUIRE(N % 8 == 0 && K % 8 == 0, MOE_ERR_UNSUPPORTED,
+              "grouped gemm: N (%lld) and K (%lld) must be multiples of 8", (long long)N, (long long)K);
+  MOE_REQUIRE(aligned16(a) && aligned16(b), MOE_ERR_INVALID, "grouped gemm: operands must be 16-byte aligned");
+  return MOE_OK;
+}
+
+}  // namespace
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up, const int32_t* offs, int64_t G,
+                                           int64_t M, int64_t H, int64_t I, void* act, void* pre, void* stream) {
+  int rc = check_common(xp, w_gate_up, offs, G, M, 2 * I, H);
+  if (rc) return rc;
+  MOE_REQUIRE(act && aligned16(act) && (!pre || aligned16(pre)), MOE_ERR_INVALID, "swiglu fwd: bad output pointer");
+  if (M == 0) return MOE_OK;
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(xp);
+  p.B = static_cast<const bf16_t*>(w_gate_up);
+  p.C = act;
+  p.C2 = pre;
+  p.offs = offs;
+  p.G = static_cast<int>(G);
+  p.rows = p.M = static_cast<int>(M);
+  p.N = static_cast<int>(2 * I);
+  p.K = static_cast<int>(H);
+  p.lda = H;
+  p.ldb = H;
+  p.ldc = I;
+  p.ldp = 2 * I;
+  p.stride_bg = 2 * I * H;
+  p.swiglu_I = static_cast<int>(I);
+  p.n_tiles = static_cast<int>((2 * I + kBN - 1) / kBN);
+  // Each tile covers BN/2 act columns; the gate/up pairing needs I in whole sub-tiles.
+  p.n_tiles = static_cast<int>((I + kBN / 2 - 1) / (kBN / 2));
+  return launch<MODE_MG, true, EPI_SWIGLU_FWD>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
+}
+
+extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t* offs, int64_t G, int64_t M, int64_t N,
+                                    int64_t K, void* c, void* stream) {
+  int rc = check_common(a, w, offs, G, M, N, K);
+  if (rc) return rc;
+  MOE_REQUIRE(c && aligned16(c), MOE_ERR_INVALID, "grouped gemm fwd: bad output pointer");
+  if (M == 0) return MOE_OK;
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(a);
+  p.B = static_cast<const bf16_t*>(w);
+  p.C = c;
+  p.offs = offs;
+  p.G = static_cast<int>(G);
+  p.rows = p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.lda = K;
+  p.ldb = K;
+  p.ldc = N;
+  p.stride_bg = N * K;
+  p.n_tiles = static_cast<int>((N + kBN - 1) / kBN);
+  return launch<MODE_MG, true, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_fwd");
+}
+
+// Router logits: f32 output, single group.
+extern "C" int moe_router_logits_fwd(const void* x, const void* wr, float* logits, int64_t T, int64_t H, int64_t E,
+                                     void* stream) {
+  int rc = check_common(x, wr, nullptr, 1, T, E, H);
+  if (rc) return rc;
+  MOE_REQUIRE(logits && aligned16(logits), MOE_ERR_INVALID, "router logits: bad output pointer");
+  if (T == 0) return MOE_OK;
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(x);
+  p.B = static_cast<const bf16_t*>(wr);
+  p.C = logits;
+  p.offs = nullptr;
+  p.G = 1;
+  p.rows = p.M = static_cast<int>(T);
+  p.N = static_cast<int>(E);
+  p.K = static_cast<int>(H);
+  p.lda = H;
+  p.ldb = H;
+  p.ldc = E;
+  p.n_tiles = static_cast<int>((E + kBN - 1) / kBN);
+  return launch<MODE_MG, true, EPI_F32>(p, as_stream(stream), "moe_router_logits_fwd");
+}
+
+extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32_t* offs, int64_t G, int64_t M,
+                                      int64_t N, int64_t K, void* da, void* stream) {
+  // da[M,K] = dc[M,N] . w[g] (w [G,N,K]): GEMM-internal reduction over N, output width K.
+  int rc = check_common(dc, w, offs, G, M, K, N);
+  if (rc) return rc;
+  MOE_REQUIRE(da && aligned16(da), MOE_ERR_INVALID, "grouped gemm dgrad: bad output pointer");
+  if (M == 0) return MOE_OK;
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(dc);
+  p.B = static_cast<const bf16_t*>(w);
+  p.C = da;
+  p.offs = offs;
+  p.G = static_cast<int>(G);
+  p.rows = p.M = static_cast<int>(M);
+  p.N = static_cast<int>(K);
+  p.K = static_cast<int>(N);
+  p.lda = N;
+  p.ldb = K;
+  p.ldc = K;
+  p.stride_bg = N * K;
+  p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
+  return launch<MODE_MG, false, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
+}
+
+extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down, const void* pre,
+                                                 const int32_t* offs, int64_t G, int64_t M, int64_t H, int64_t I,
+                                                 void* d_pre, void* stream) {
+  // d_act[M,I] = dy[M,H] . w_down[g] (w_down [G,H,I]); fused SwiGLU backward.
+  int rc = check_common(dy, w_down, offs, G, M, I, H);
+  if (rc) return rc;
+  MOE_REQUIRE(pre && d_pre && aligned16(pre) && aligned16(d_pre), MOE_ERR_INVALID,
+              "dgrad swiglu: bad pre/d_pre pointer");
+  if (M == 0) return MOE_OK;
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(dy);
+  p.B = static_cast<const bf16_t*>(w_down);
+  p.C = d_pre;
+  p.P = static_cast<const bf16_t*>(pre);
+  p.offs = offs;
+  p.G = static_cast<int>(G);
+  p.rows = p.M = static_cast<int>(M);
+  p.N = static_cast<int>(I);
+  p.K = static_cast<int>(H);
+  p.lda = H;
+  p.ldb = I;
+  p.ldc = 2 * I;
+  p.ldp = 2 * I;
+  p.stride_bg = H * I;
+  p.n_tiles = static_cast<int>((I + kBN - 1) / kBN);
+  return launch<MODE_MG, false, EPI_SWIGLU_BWD>(p, as_stream(stream), "moe_grouped_gemm_dgrad_swiglu_bwd");
+}
+
+extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
+                                      int64_t N, int64_t K, void* dw, int dw_is_f32, int accumulate, void* stream) {
+  // dw[g][N,K] = dc[rows g, N]^T . a[rows g, K]: GEMM-internal output N x K, reduction over rows.
+  int rc = check_common(dc, a, offs, G, M, N, K);
+  if (rc) return rc;
+  MOE_REQUIRE(dw && aligned16(dw), MOE_ERR_INVALID, "grouped gemm wgrad: bad output pointer");
+  GemmParams p{};
+  p.A = static_cast<const bf16_t*>(dc);
+  p.B = static_cast<const bf16_t*>(a);
+  p.C = dw;
+  p.offs = offs;
+  p.G = static_cast<int>(G);
+  p.rows = static_cast<int>(M);
+  p.M = static_cast<int>(N);
+  p.N = static_cast<int>(K);
+  p.K = 0;
+  p.lda = N;
+  p.ldb = K;
+  p.ldc = K;
+  p.ldp = dw_is_f32 ? 1 : 0;
+  p.stride_cg = N * K;
+  p.accumulate = accumulate ? 1 : 0;
+  p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
+  return launch<MODE_KG, false, EPI_WGRAD>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
+}

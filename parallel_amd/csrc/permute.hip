@@ -1,0 +1,312 @@
+// Token permutation into expert-contiguous (or owner-rank-contiguous) order.
+//
+// A stable counting sort of the S = T*k routed slots by bucket = id / divisor,
+// in three small launches plus one bandwidth-bound row gather:
+//   1. count:   each block histograms a CHUNK of slots in LDS (integer
+//               atomics, so counts are exact and order-free);
+//   2. scan:    one block turns the [blocks x buckets] histogram into the
+//               first sorted position of every (block, bucket) pair, plus the
+//               per-bucket counts and inclusive offsets;
+//   3. scatter: each block re-walks its chunk 256 slots at a time; a wave
+//               finds equal keys with one ballot per key bit, ranks a slot by
+//               the popcount of equal-key lanes below it, and waves are
+//               ordered through per-round LDS counters, which keeps the sort
+//               stable;
+//   4. gather:  one wave per sorted row copies hidden[perm/k] (16-byte lanes).
+// Sentinel slots (bucket >= num_buckets) land after every real bucket.
+//
+// Reference: TF/integrations/moe.py:389-437 (sort/gather/histc/cumsum,
+// sentinel handling) and parallel/parallel/engine/model_parallel/
+// token_dispatch.py:101-125 (argsort by owner, bincount splits, index_select).
+#include "common.h"
+
+namespace moe {
+
+constexpr int kChunk = 2048;       // slots per block in count/scatter
+constexpr int kPermThreads = 256;  // 4 waves
+constexpr int kMaxBuckets = 1024;  // real buckets; +1 for the sentinel bucket
+
+__device__ __forceinline__ int bucket_of(int64_t id, int64_t divisor, int nb) {
+  int64_t b = id / divisor;
+  return (b < 0 || b >= nb) ? nb : static_cast<int>(b);
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_count_kernel(const int64_t* __restrict__ ids, int S,
+                                                                      int64_t divisor, int nb,
+                                                                      int32_t* __restrict__ hist) {
+  __shared__ int h[kMaxBuckets + 1];
+  const int nb1 = nb + 1;
+  for (int i = threadIdx.x; i < nb1; i += kPermThreads) h[i] = 0;
+  __syncthreads();
+  const int begin = blockIdx.x * kChunk;
+  const int end = min(begin + kChunk, S);
+  for (int s = begin + threadIdx.x; s < end; s += kPermThreads) atomicAdd(&h[bucket_of(ids[s], divisor, nb)], 1);
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb1; i += kPermThreads) hist[static_cast<int64_t>(blockIdx.x) * nb1 + i] = h[i];
+}
+
+// hist[b][e] (counts) -> base[b][e] (first sorted position), in place.
+__global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict__ hist, int nblk, int nb,
+                                                            int32_t* __restrict__ counts,
+                                                            int32_t* __restrict__ offsets) {
+  __shared__ int tot[kMaxBuckets + 1];
+  __shared__ int wsum[16];
+  const int nb1 = nb + 1;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid >> 6;
+  // Column prefix over blocks (per bucket), exclusive.
+  for (int e = tid; e < nb1; e += blockDim.x) {
+    int run = 0;
+    for (int b = 0; b < nblk; ++b) {
+      int64_t o = static_cast<int64_t>(b) * nb1 + e;
+      int c = hist[o];
+      hist[o] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  // Exclusive scan over buckets (nb1 <= 1025 entries; two passes of 1024).
+  __shared__ int start[kMaxBuckets + 1];
+  int carry = 0;
+  for (int base = 0; base < nb1; base += 1024) {
+    int e = base + tid;
+    int v = e < nb1 ? tot[e] : 0;
+    int incl = wave_inclusive_scan(v);
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int wprefix = 0;
+    for (int w = 0; w < wave; ++w) wprefix += wsum[w];
+    if (e < nb1) start[e] = carry + wprefix + incl - v;
+    __syncthreads();
+    int chunk_total = 0;
+    for (int w = 0; w < 16; ++w) chunk_total += wsum[w];
+    carry += chunk_total;
+    __syncthreads();
+  }
+  for (int e = tid; e < nb1; e += blockDim.x) {
+    if (e < nb) {
+      counts[e] = tot[e];
+      offsets[e] = start[e] + tot[e];
+    }
+    for (int b = 0; b < nblk; ++b) hist[static_cast<int64_t>(b) * nb1 + e] += start[e];
+  }
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(const int64_t* __restrict__ ids, int S,
+                                                                        int64_t divisor, int nb,
+                                                                        const int32_t* __restrict__ base,
+                                                                        int32_t* __restrict__ perm,
+                                                                        int32_t* __restrict__ pos_of_slot) {
+  __shared__ int running[kMaxBuckets + 1];
+  __shared__ int wave_cnt[kPermThreads / kWave][kMaxBuckets + 1];
+  const int nb1 = nb + 1;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < nb1; i += kPermThreads) {
+    running[i] = base[static_cast<int64_t>(blockIdx.x) * nb1 + i];
+#pragma unroll
+    for (int w = 0; w < kPermThreads / kWave; ++w) wave_cnt[w][i] = 0;
+  }
+  __syncthreads();
+  int nbits = 1;
+  while ((1 << nbits) < nb1) ++nbits;
+  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int begin = blockIdx.x * kChunk;
+  const int end = min(begin + kChunk, S);
+  for (int r0 = begin; r0 < end; r0 += kPermThreads) {
+    const int s = r0 + threadIdx.x;
+    const bool live = s < end;
+    const int key = live ? bucket_of(ids[s], divisor, nb) : 0;
+    // Lanes holding the same key: intersect one ballot per key bit.
+    unsigned long long match = __ballot(live);
+#pragma unroll 1
+    for (int b = 0; b < nbits; ++b) {
+      unsigned long long set = __ballot(live && ((key >> b) & 1));
+      match &= ((key >> b) & 1) ? set : ~set;
+    }
+    const int rank = __popcll(match & lt_mask);
+    const bool leader = live && rank == 0;
+    if (leader) wave_cnt[wave][key] = __popcll(match);
+    __syncthreads();
+    if (live) {
+      int pos = running[key] + rank;
+      for (int w = 0; w < wave; ++w) pos += wave_cnt[w][key];
+      if (pos >= 0 && pos < S) {  // always true for a consistent histogram; never write outside
+        perm[pos] = s;
+        pos_of_slot[s] = pos;
+      }
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&running[key], wave_cnt[wave][key]);
+      wave_cnt[wave][key] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// permuted[pos] = hidden[perm[pos] / k] for pos < n_valid, zero after.
+__global__ __launch_bounds__(kPermThreads) void gather_rows_kernel(const bf16_t* __restrict__ hidden, int H,
+                                                                    const int32_t* __restrict__ perm, int S, int k,
+                                                                    const int32_t* __restrict__ n_valid_ptr,
+                                                                    bf16_t* __restrict__ out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n_valid = *n_valid_ptr;
+  const int nchunk = H / 8;
+  for (int pos = blockIdx.x * (kPermThreads / kWave) + (threadIdx.x >> 6); pos < S;
+       pos += gridDim.x * (kPermThreads / kWave)) {
+    uint4* dst = reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos) * H);
+    if (pos < n_valid) {
+      const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<int64_t>(perm[pos] / k) * H);
+      for (int c = lane; c < nchunk; c += kWave) dst[c] = src[c];
+    } else {
+      for (int c = lane; c < nchunk; c += kWave) dst[c] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+__global__ void dispatch_meta_kernel(const int64_t* __restrict__ ids, const float* __restrict__ scores,
+                                     const int32_t* __restrict__ perm, int S, int64_t divisor,
+                                     int64_t* __restrict__ local_ids, float* __restrict__ routed_scores) {
+  for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < S; pos += gridDim.x * blockDim.x) {
+    int s = perm[pos];
+    if (local_ids) {
+      int64_t id = ids[s];
+      local_ids[pos] = id - (id / divisor) * divisor;
+    }
+    if (routed_scores) routed_scores[pos] = scores[s];
+  }
+}
+
+// d_hidden[t] = sum_j d_permuted[pos_of_slot[t*k+j]] (+ d_add[t]); one wave per token.
+__global__ __launch_bounds__(kPermThreads) void permute_bwd_kernel(const bf16_t* __restrict__ dperm,
+                                                                    const int32_t* __restrict__ pos_of_slot,
+                                                                    const int32_t* __restrict__ n_valid_ptr, int T,
+                                                                    int H, int k, const bf16_t* __restrict__ d_add,
+                                                                    bf16_t* __restrict__ dh) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n_valid = *n_valid_ptr;
+  const int nchunk = H / 8;
+  for (int t = blockIdx.x * (kPermThreads / kWave) + (threadIdx.x >> 6); t < T;
+       t += gridDim.x * (kPermThreads / kWave)) {
+    int pos[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) pos[j] = (j < k) ? pos_of_slot[static_cast<int64_t>(t) * k + j] : n_valid;
+    for (int c = lane; c < nchunk; c += kWave) {
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (j < k && pos[j] < n_valid) {
+          uint4 v = reinterpret_cast<const uint4*>(dperm + static_cast<int64_t>(pos[j]) * H)[c];
+          acc[0] += lo_bf16(v.x); acc[1] += hi_bf16(v.x);
+          acc[2] += lo_bf16(v.y); acc[3] += hi_bf16(v.y);
+          acc[4] += lo_bf16(v.z); acc[5] += hi_bf16(v.z);
+          acc[6] += lo_bf16(v.w); acc[7] += hi_bf16(v.w);
+        }
+      }
+      if (d_add) {
+        uint4 v = reinterpret_cast<const uint4*>(d_add + static_cast<int64_t>(t) * H)[c];
+        acc[0] += lo_bf16(v.x); acc[1] += hi_bf16(v.x);
+        acc[2] += lo_bf16(v.y); acc[3] += hi_bf16(v.y);
+        acc[4] += lo_bf16(v.z); acc[5] += hi_bf16(v.z);
+        acc[6] += lo_bf16(v.w); acc[7] += hi_bf16(v.w);
+      }
+      uint4 o;
+      o.x = pack_bf16x2(acc[0], acc[1]);
+      o.y = pack_bf16x2(acc[2], acc[3]);
+      o.z = pack_bf16x2(acc[4], acc[5]);
+      o.w = pack_bf16x2(acc[6], acc[7]);
+      reinterpret_cast<uint4*>(dh + static_cast<int64_t>(t) * H)[c] = o;
+    }
+  }
+}
+
+int row_grid(int64_t rows) {
+  int64_t b = (rows + (kPermThreads / kWave) - 1) / (kPermThreads / kWave);
+  if (b > 8192) b = 8192;
+  return static_cast<int>(b < 1 ? 1 : b);
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" size_t moe_permute_workspace_bytes(int64_t S, int64_t num_buckets) {
+  if (S < 0 || num_buckets < 1) return 0;
+  int64_t nblk = (S + kChunk - 1) / kChunk;
+  if (nblk < 1) nblk = 1;
+  return static_cast<size_t>(nblk) * static_cast<size_t>(num_buckets + 1) * sizeof(int32_t);
+}
+
+extern "C" int moe_permute_fwd(const void* hidden, int64_t T, int64_t H, const int64_t* ids, int64_t k,
+                               int64_t divisor, int64_t num_buckets, void* permuted, int32_t* perm,
+                               int32_t* pos_of_slot, int32_t* counts, int32_t* offsets, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  MOE_REQUIRE(T >= 0 && k >= 1 && k <= 16 && T * k < (1ll << 31), MOE_ERR_INVALID,
+              "permute: bad T=%lld k=%lld", (long long)T, (long long)k);
+  MOE_REQUIRE(divisor >= 1, MOE_ERR_INVALID, "permute: divisor must be >= 1");
+  MOE_REQUIRE(num_buckets >= 1 && num_buckets <= kMaxBuckets, MOE_ERR_UNSUPPORTED,
+              "permute: num_buckets=%lld outside [1,%d]", (long long)num_buckets, kMaxBuckets);
+  MOE_REQUIRE(counts && offsets && (T == 0 || (ids && perm && pos_of_slot)), MOE_ERR_INVALID, "permute: null pointer");
+  MOE_REQUIRE(!permuted || (hidden && H > 0 && H % 8 == 0 && aligned16(hidden) && aligned16(permuted)),
+              MOE_ERR_INVALID, "permute: rows need H %% 8 == 0 and 16-byte aligned buffers");
+  const int S = static_cast<int>(T * k);
+  const int nb = static_cast<int>(num_buckets);
+  const size_t need = moe_permute_workspace_bytes(S, num_buckets);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "permute: workspace %zu < %zu bytes",
+              workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  int32_t* hist = static_cast<int32_t*>(workspace);
+  const int nblk = (S + kChunk - 1) / kChunk;
+  if (nblk > 0) {
+    hipLaunchKernelGGL(permute_count_kernel, dim3(nblk), dim3(kPermThreads), 0, st, ids, S, divisor, nb, hist);
+    int rc = launch_status("moe_permute_fwd(count)");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, st, hist, nblk, nb, counts, offsets);
+  int rc = launch_status("moe_permute_fwd(scan)");
+  if (rc) return rc;
+  if (nblk == 0) return MOE_OK;
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nblk), dim3(kPermThreads), 0, st, ids, S, divisor, nb, hist, perm,
+                     pos_of_slot);
+  rc = launch_status("moe_permute_fwd(scatter)");
+  if (rc) return rc;
+  if (permuted) {
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(row_grid(S)), dim3(kPermThreads), 0, st,
+                       static_cast<const bf16_t*>(hidden), static_cast<int>(H), perm, S, static_cast<int>(k),
+                       offsets + (nb - 1), static_cast<bf16_t*>(permuted));
+    rc = launch_status("moe_permute_fwd(gather)");
+  }
+  return rc;
+}
+
+extern "C" int moe_dispatch_meta(const int64_t* ids, const float* scores, const int32_t* perm, int64_t S,
+                                 int64_t divisor, int64_t* local_ids, float* routed_scores, void* stream) {
+  MOE_REQUIRE(S >= 0 && S < (1ll << 31) && divisor >= 1, MOE_ERR_INVALID, "dispatch meta: bad sizes");
+  if (S == 0) return MOE_OK;
+  MOE_REQUIRE(ids && perm && (!routed_scores || scores), MOE_ERR_INVALID, "dispatch meta: null pointer");
+  int blocks = static_cast<int>((S + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(dispatch_meta_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), ids, scores, perm,
+                     static_cast<int>(S), divisor, local_ids, routed_scores);
+  return launch_status("moe_dispatch_meta");
+}
+
+extern "C" int moe_permute_bwd(const void* d_permuted, const int32_t* pos_of_slot, const int32_t* offsets,
+                               int64_t num_buckets, int64_t T, int64_t H, int64_t k, const void* d_add,
+                               void* d_hidden, void* stream) {
+  MOE_REQUIRE(T >= 0 && k >= 1 && k <= 16 && H > 0 && H % 8 == 0, MOE_ERR_INVALID,
+              "permute bwd: bad sizes T=%lld H=%lld k=%lld", (long long)T, (long long)H, (long long)k);
+  MOE_REQUIRE(num_buckets >= 1, MOE_ERR_INVALID, "permute bwd: num_buckets must be >= 1");
+  if (T == 0) return MOE_OK;
+  MOE_REQUIRE(d_permuted && pos_of_slot && offsets && d_hidden, MOE_ERR_INVALID, "permute bwd: null pointer");
+  MOE_REQUIRE(aligned16(d_permuted) && aligned16(d_hidden) && (!d_add || aligned16(d_add)), MOE_ERR_INVALID,
+              "permute bwd: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(permute_bwd_kernel, dim3(row_grid(T)), dim3(kPermThreads), 0, as_stream(stream),
+                     static_cast<const bf16_t*>(d_permuted), pos_of_slot, offsets + (num_buckets - 1),
+                     static_cast<int>(T), static_cast<int>(H), static_cast<int>(k),
+                     static_cast<const bf16_t*>(d_add), static_cast<bf16_t*>(d_hidden));
+  return launch_status("moe_permute_bwd");
+}

@@ -1,0 +1,522 @@
+"""torch.library ops over the gfx950 C-ABI kernels, with fake kernels and autograd.
+
+Every op runs on torch's current stream of the input's device and allocates
+its outputs and workspaces from the caching allocator; none synchronises with
+the host.  There is no CPU implementation: CPU tensors raise ``ValueError``.
+
+Ops (namespace ``parallel_amd``):
+  router_fwd / router_bwd          router GEMM + top-k softmax (+ backward)
+  router_topk                      top-k softmax of given fp32 logits
+  aux_loss_fwd / aux_loss_bwd      Switch load-balancing loss
+  permute_fwd                      stable sort of routed slots + row gather
+  experts_fwd / experts_bwd        permute -> SwiGLU grouped GEMMs -> combine
+  dispatch_fwd / dispatch_bwd      owner-rank sort for TokenDispatcher
+  combine_rows_fwd / _bwd          gather-form index_add back to source tokens
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import call, ptr
+
+LIB = "parallel_amd"
+BF16 = torch.bfloat16
+
+
+# ---------------------------------------------------------------- validation
+
+
+def _require_gpu(*tensors: Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                f"parallel_amd kernels run on the GPU only; got a tensor on {t.device} "
+                "(there is no CPU implementation)"
+            )
+
+
+def _require_bf16(name: str, t: Tensor) -> None:
+    if t.dtype != BF16:
+        raise ValueError(f"{name} must be bfloat16 for the MFMA kernels, got {t.dtype}")
+
+
+def _stream(t: Tensor) -> int:
+    return _lib.stream_of(t)
+
+
+def _ws(nbytes: int, device) -> Tensor:
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+def _ids64(t: Tensor) -> Tensor:
+    return t.to(torch.int64).contiguous()
+
+
+# ------------------------------------------------------------------- router
+
+
+@torch.library.custom_op(f"{LIB}::router_topk", mutates_args=())
+def router_topk(logits: Tensor, top_k: int, norm_topk_prob: bool) -> tuple[Tensor, Tensor]:
+    """(scores [T,k] f32, indices [T,k] int64) of softmax(logits) (TF modeling_qwen3_moe.py:261-265)."""
+    _require_gpu(logits)
+    logits = logits.float().contiguous()
+    T, E = logits.shape
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=logits.device)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=logits.device)
+    call("moe_router_topk_fwd", ptr(logits), ptr(scores), ptr(idx), T, E, top_k, int(norm_topk_prob),
+         _stream(logits))
+    return scores, idx
+
+
+@router_topk.register_fake
+def _(logits, top_k, norm_topk_prob):
+    T = logits.shape[0]
+    return logits.new_empty(T, top_k, dtype=torch.float32), logits.new_empty(T, top_k, dtype=torch.int64)
+
+
+@torch.library.custom_op(f"{LIB}::router_fwd", mutates_args=())
+def router_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool,
+               logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """Qwen3MoeTopKRouter.forward (TF modeling_qwen3_moe.py:258-267) with fp32 logits.
+
+    ``logit_bias`` [E] (fp32, not differentiated) is added to the logits before
+    the softmax; the reference router has none, the imbalanced benchmark
+    harness uses it."""
+    _require_gpu(x, weight)
+    _require_bf16("router input", x)
+    _require_bf16("router weight", weight)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    T, H = x.shape
+    E = weight.shape[0]
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    s = _stream(x)
+    call("moe_router_logits_fwd", ptr(x), ptr(weight), ptr(logits), T, H, E, s, tag="router_logits")
+    if logit_bias is not None:
+        logits.add_(logit_bias.to(device=x.device, dtype=torch.float32))
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=x.device)
+    call("moe_router_topk_fwd", ptr(logits), ptr(scores), ptr(idx), T, E, top_k, int(norm_topk_prob), s,
+         tag="router_topk")
+    return logits, scores, idx
+
+
+@router_fwd.register_fake
+def _(x, weight, top_k, norm_topk_prob, logit_bias=None):
+    T, E = x.shape[0], weight.shape[0]
+    return (x.new_empty(T, E, dtype=torch.float32), x.new_empty(T, top_k, dtype=torch.float32),
+            x.new_empty(T, top_k, dtype=torch.int64))
+
+
+@torch.library.custom_op(f"{LIB}::router_bwd", mutates_args=())
+def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
+               d_scores: Tensor | None, norm_topk_prob: bool) -> tuple[Tensor, Tensor]:
+    """(dx [T,H] bf16, dweight [E,H] bf16) through top-k/renorm/softmax and the router GEMM."""
+    x = x.contiguous()
+    weight = weight.contiguous()
+    T, H = x.shape
+    E = weight.shape[0]
+    k = indices.shape[1]
+    s = _stream(x)
+    if d_logits is not None:
+        dl = d_logits.float().contiguous().clone()
+    else:
+        dl = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    dl_bf16 = torch.empty(T, E, dtype=BF16, device=x.device)
+    if d_scores is None:
+        d_scores = torch.zeros(T, k, dtype=torch.float32, device=x.device)
+    d_scores = d_scores.float().contiguous()
+    call("moe_router_topk_bwd", ptr(logits), ptr(indices), ptr(d_scores), T, E, k, int(norm_topk_prob), ptr(dl),
+         int(d_logits is not None), ptr(dl_bf16), s, tag="router_topk_bwd")
+    dx = torch.empty(T, H, dtype=BF16, device=x.device)
+    call("moe_grouped_gemm_dgrad", ptr(dl_bf16), ptr(weight), None, 1, T, E, H, ptr(dx), s, tag="router_dgrad")
+    dw = torch.empty(E, H, dtype=weight.dtype, device=x.device)
+    call("moe_grouped_gemm_wgrad", ptr(dl_bf16), ptr(x), None, 1, T, E, H, ptr(dw), 0, 0, s, tag="router_wgrad")
+    return dx, dw
+
+
+@router_bwd.register_fake
+def _(x, weight, logits, indices, d_logits, d_scores, norm_topk_prob):
+    return torch.empty_like(x), torch.empty_like(weight)
+
+
+def _router_setup(ctx, inputs, output):
+    x, weight, top_k, norm, _bias = inputs
+    logits, _, idx = output
+    ctx.save_for_backward(x, weight, logits, idx)
+    ctx.norm = norm
+    ctx.mark_non_differentiable(idx)
+
+
+def _router_backward(ctx, d_logits, d_scores, _d_idx):
+    x, weight, logits, idx = ctx.saved_tensors
+    dx, dw = router_bwd(x, weight, logits, idx, d_logits, d_scores, ctx.norm)
+    return dx, dw, None, None, None
+
+
+router_fwd.register_autograd(_router_backward, setup_context=_router_setup)
+
+
+# ----------------------------------------------------------------- aux loss
+
+
+@torch.library.custom_op(f"{LIB}::aux_loss_fwd", mutates_args=())
+def aux_loss_fwd(logits: Tensor, token_weight: Tensor | None, num_experts: int, top_k: int) -> tuple[Tensor, Tensor]:
+    """(aux scalar f32, stats [E+1] = per-expert routed counts and the token total)."""
+    _require_gpu(logits, token_weight)
+    logits = logits.float().contiguous()
+    T, E = logits.shape
+    if E != num_experts:
+        raise ValueError(f"router logits have {E} experts, expected {num_experts}")
+    tw = None if token_weight is None else token_weight.float().contiguous()
+    aux = torch.empty((), dtype=torch.float32, device=logits.device)
+    stats = torch.empty(E + 1, dtype=torch.float32, device=logits.device)
+    nbytes = _lib.load().moe_aux_loss_workspace_bytes(T, E)
+    ws = _ws(nbytes, logits.device)
+    call("moe_aux_loss_fwd", ptr(logits), ptr(tw), T, E, top_k, ptr(aux), ptr(stats), ptr(ws), ws.numel(),
+         _stream(logits), tag="aux_fwd")
+    return aux, stats
+
+
+@aux_loss_fwd.register_fake
+def _(logits, token_weight, num_experts, top_k):
+    return logits.new_empty((), dtype=torch.float32), logits.new_empty(num_experts + 1, dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{LIB}::aux_loss_bwd", mutates_args=())
+def aux_loss_bwd(logits: Tensor, token_weight: Tensor | None, stats: Tensor, d_aux: Tensor) -> Tensor:
+    logits = logits.float().contiguous()
+    T, E = logits.shape
+    tw = None if token_weight is None else token_weight.float().contiguous()
+    d_aux = d_aux.float().reshape(1).contiguous()
+    dl = torch.empty(T, E, dtype=torch.float32, device=logits.device)
+    call("moe_aux_loss_bwd", ptr(logits), ptr(tw), ptr(stats), ptr(d_aux), T, E, ptr(dl), 0, _stream(logits),
+         tag="aux_bwd")
+    return dl
+
+
+@aux_loss_bwd.register_fake
+def _(logits, token_weight, stats, d_aux):
+    return torch.empty_like(logits, dtype=torch.float32)
+
+
+def _aux_setup(ctx, inputs, output):
+    logits, token_weight, _, _ = inputs
+    _, stats = output
+    ctx.save_for_backward(logits, token_weight, stats)
+    ctx.logits_dtype = logits.dtype
+    ctx.mark_non_differentiable(stats)
+
+
+def _aux_backward(ctx, d_aux, _d_stats):
+    logits, token_weight, stats = ctx.saved_tensors
+    dl = aux_loss_bwd(logits, token_weight, stats, d_aux)
+    return dl.to(ctx.logits_dtype), None, None, None
+
+
+aux_loss_fwd.register_autograd(_aux_backward, setup_context=_aux_setup)
+
+
+# ------------------------------------------------------------------ permute
+
+
+@torch.library.custom_op(f"{LIB}::permute_fwd", mutates_args=())
+def permute_fwd(hidden: Tensor, ids: Tensor, divisor: int, num_buckets: int,
+                gather_rows: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Stable sort of slots by ids // divisor.
+
+    Returns (permuted rows [S,H] or empty, perm [S] int32, pos_of_slot [S] int32,
+    counts [nb] int32, offsets [nb] int32); slots whose bucket is >= num_buckets
+    are sentinels placed last (TF integrations/moe.py:389-437).
+    """
+    _require_gpu(hidden, ids)
+    T = hidden.shape[0]
+    H = hidden.shape[1] if hidden.dim() == 2 else 0
+    if ids.dim() != 2 or ids.shape[0] != T:
+        raise ValueError(f"ids must be [T, k] with T={T}, got {tuple(ids.shape)}")
+    k = ids.shape[1]
+    S = T * k
+    dev = hidden.device
+    ids = _ids64(ids)
+    perm = torch.empty(S, dtype=torch.int32, device=dev)
+    pos = torch.empty(S, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_buckets, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_buckets, dtype=torch.int32, device=dev)
+    if gather_rows:
+        _require_bf16("hidden", hidden)
+        hidden = hidden.contiguous()
+        out = torch.empty(S, H, dtype=hidden.dtype, device=dev)
+    else:
+        out = torch.empty(0, dtype=BF16, device=dev)
+    ws = _ws(_lib.load().moe_permute_workspace_bytes(S, num_buckets), dev)
+    call("moe_permute_fwd", ptr(hidden) if gather_rows else None, T, H, ptr(ids), k, divisor, num_buckets,
+         ptr(out) if gather_rows else None, ptr(perm), ptr(pos), ptr(counts), ptr(offsets), ptr(ws), ws.numel(),
+         _stream(ids))
+    return out, perm, pos, counts, offsets
+
+
+@permute_fwd.register_fake
+def _(hidden, ids, divisor, num_buckets, gather_rows):
+    S = ids.shape[0] * ids.shape[1]
+    rows = hidden.new_empty(S, hidden.shape[1]) if gather_rows else hidden.new_empty(0)
+    i32 = dict(dtype=torch.int32)
+    return (rows, ids.new_empty(S, **i32), ids.new_empty(S, **i32), ids.new_empty(num_buckets, **i32),
+            ids.new_empty(num_buckets, **i32))
+
+
+# ------------------------------------------------------------------ experts
+
+
+def _check_experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
+                   down_proj: Tensor) -> tuple[int, int, int, int, int]:
+    _require_gpu(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
+    if hidden.dim() != 2:
+        raise ValueError(f"hidden states must be [tokens, hidden], got {tuple(hidden.shape)}")
+    if top_k_index.shape != top_k_weights.shape or top_k_index.dim() != 2 or top_k_index.shape[0] != hidden.shape[0]:
+        raise ValueError("top_k_index and top_k_weights must both be [tokens, k]")
+    T, H = hidden.shape
+    k = top_k_index.shape[1]
+    E, I2, H2 = gate_up_proj.shape
+    if H2 != H or I2 % 2 or tuple(down_proj.shape) != (E, H, I2 // 2):
+        raise ValueError(
+            f"expert weights do not match: gate_up_proj {tuple(gate_up_proj.shape)}, "
+            f"down_proj {tuple(down_proj.shape)}, hidden {H}"
+        )
+    for name, t in (("hidden states", hidden), ("gate_up_proj", gate_up_proj), ("down_proj", down_proj)):
+        _require_bf16(name, t)
+    return T, H, k, E, I2 // 2
+
+
+@torch.library.custom_op(f"{LIB}::experts_fwd", mutates_args=())
+def experts_fwd(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
+                down_proj: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """grouped_mm_experts_forward (TF integrations/moe.py:377-478) on gfx950.
+
+    Returns (out [T,H], and for the backward: xp [S,H], pre [S,2I], act [S,I],
+    y [S,H], pos_of_slot [S] int32, offsets [E] int32).
+    """
+    T, H, k, E, I = _check_experts(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
+    S = T * k
+    dev = hidden.device
+    s = _stream(hidden)
+    hidden = hidden.contiguous()
+    ids = _ids64(top_k_index)
+    w = top_k_weights.float().contiguous()
+    gu = gate_up_proj.contiguous()
+    dn = down_proj.contiguous()
+    xp = torch.empty(S, H, dtype=BF16, device=dev)
+    perm = torch.empty(S, dtype=torch.int32, device=dev)
+    pos = torch.empty(S, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E, dtype=torch.int32, device=dev)
+    ws = _ws(_lib.load().moe_permute_workspace_bytes(S, E), dev)
+    call("moe_permute_fwd", ptr(hidden), T, H, ptr(ids), k, 1, E, ptr(xp), ptr(perm), ptr(pos), ptr(counts),
+         ptr(offsets), ptr(ws), ws.numel(), s, tag="permute_fwd")
+    act = torch.empty(S, I, dtype=BF16, device=dev)
+    pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
+    call("moe_grouped_gemm_swiglu_fwd", ptr(xp), ptr(gu), ptr(offsets), E, S, H, I, ptr(act), ptr(pre), s,
+         tag="up_fwd")
+    y = torch.empty(S, H, dtype=BF16, device=dev)
+    call("moe_grouped_gemm_fwd", ptr(act), ptr(dn), ptr(offsets), E, S, H, I, ptr(y), s, tag="down_fwd")
+    out = torch.empty(T, H, dtype=BF16, device=dev)
+    call("moe_combine_fwd", ptr(y), ptr(pos), ptr(offsets), E, ptr(w), T, H, k, ptr(out), s, tag="combine_fwd")
+    return out, xp, pre, act, y, pos, offsets
+
+
+@experts_fwd.register_fake
+def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj):
+    T, H = hidden.shape
+    S = T * top_k_index.shape[1]
+    E, I2, _ = gate_up_proj.shape
+    i32 = dict(dtype=torch.int32)
+    return (hidden.new_empty(T, H), hidden.new_empty(S, H), hidden.new_empty(S, I2), hidden.new_empty(S, I2 // 2),
+            hidden.new_empty(S, H), hidden.new_empty(S, **i32), hidden.new_empty(E, **i32))
+
+
+@torch.library.custom_op(f"{LIB}::experts_bwd", mutates_args=())
+def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
+                pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor,
+                offsets: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d_hidden [T,H], d_weights [T,k] f32, d_gate_up_proj, d_down_proj)."""
+    T, k = top_k_weights.shape
+    E, I2, H = gate_up_proj.shape
+    I = I2 // 2
+    S = T * k
+    dev = d_out.device
+    s = _stream(d_out)
+    d_out = d_out.to(BF16).contiguous()
+    w = top_k_weights.float().contiguous()
+    dy = torch.empty(S, H, dtype=BF16, device=dev)
+    d_w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    call("moe_combine_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
+         ptr(d_w), s, tag="combine_bwd")
+    d_pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
+    call("moe_grouped_gemm_dgrad_swiglu_bwd", ptr(dy), ptr(down_proj), ptr(pre), ptr(offsets), E, S, H, I,
+         ptr(d_pre), s, tag="down_dgrad")
+    d_down = torch.empty_like(down_proj)
+    call("moe_grouped_gemm_wgrad", ptr(dy), ptr(act), ptr(offsets), E, S, H, I, ptr(d_down), 0, 0, s,
+         tag="down_wgrad")
+    d_xp = torch.empty(S, H, dtype=BF16, device=dev)
+    call("moe_grouped_gemm_dgrad", ptr(d_pre), ptr(gate_up_proj), ptr(offsets), E, S, 2 * I, H, ptr(d_xp), s,
+         tag="up_dgrad")
+    d_gu = torch.empty_like(gate_up_proj)
+    call("moe_grouped_gemm_wgrad", ptr(d_pre), ptr(xp), ptr(offsets), E, S, 2 * I, H, ptr(d_gu), 0, 0, s,
+         tag="up_wgrad")
+    d_hidden = torch.empty(T, H, dtype=BF16, device=dev)
+    call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, None, ptr(d_hidden), s,
+         tag="permute_bwd")
+    return d_hidden, d_w, d_gu, d_down
+
+
+@experts_bwd.register_fake
+def _(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets):
+    return (torch.empty_like(d_out), top_k_weights.new_empty(top_k_weights.shape, dtype=torch.float32),
+            torch.empty_like(gate_up_proj), torch.empty_like(down_proj))
+
+
+def _experts_setup(ctx, inputs, output):
+    hidden, top_k_index, top_k_weights, gate_up_proj, down_proj = inputs
+    _, xp, pre, act, y, pos, offsets = output
+    ctx.save_for_backward(top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos, offsets)
+    ctx.weights_dtype = top_k_weights.dtype
+    ctx.hidden_dtype = hidden.dtype
+    ctx.mark_non_differentiable(xp, pre, act, y, pos, offsets)
+
+
+def _experts_backward(ctx, d_out, *_unused):
+    w, gu, dn, xp, pre, act, y, pos, offsets = ctx.saved_tensors
+    if d_out is None:
+        return None, None, None, None, None
+    d_hidden, d_w, d_gu, d_dn = experts_bwd(d_out, w, gu, dn, xp, pre, act, y, pos, offsets)
+    return d_hidden.to(ctx.hidden_dtype), None, d_w.to(ctx.weights_dtype), d_gu, d_dn
+
+
+experts_fwd.register_autograd(_experts_backward, setup_context=_experts_setup)
+
+
+def experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
+            down_proj: Tensor) -> Tensor:
+    """Differentiable expert layer output [T,H] (TF integrations/moe.py:377-478 contract)."""
+    return experts_fwd(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)[0]
+
+
+# ------------------------------------------------------- token dispatch ops
+
+
+@torch.library.custom_op(f"{LIB}::dispatch_fwd", mutates_args=())
+def dispatch_fwd(hidden: Tensor, global_indices: Tensor, scores: Tensor, local_count: int,
+                 ep_size: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Owner-major send buffers of TokenDispatcher.dispatch (token_dispatch.py:101-125).
+
+    Returns (send_hidden [S,H], send_experts [S] int64 (local ids),
+    send_scores [S], source_tokens [S] int64, pos_of_slot [S] int32,
+    counts [ep] int32 = send splits).
+    """
+    _require_gpu(hidden, global_indices, scores)
+    _require_bf16("hidden states", hidden)
+    T, H = hidden.shape
+    k = global_indices.shape[1]
+    S = T * k
+    dev = hidden.device
+    s = _stream(hidden)
+    hidden = hidden.contiguous()
+    ids = _ids64(global_indices)
+    sc = scores.float().contiguous()
+    send_hidden = torch.empty(S, H, dtype=hidden.dtype, device=dev)
+    perm = torch.empty(S, dtype=torch.int32, device=dev)
+    pos = torch.empty(S, dtype=torch.int32, device=dev)
+    counts = torch.empty(ep_size, dtype=torch.int32, device=dev)
+    offsets = torch.empty(ep_size, dtype=torch.int32, device=dev)
+    ws = _ws(_lib.load().moe_permute_workspace_bytes(S, ep_size), dev)
+    call("moe_permute_fwd", ptr(hidden), T, H, ptr(ids), k, local_count, ep_size, ptr(send_hidden), ptr(perm),
+         ptr(pos), ptr(counts), ptr(offsets), ptr(ws), ws.numel(), s)
+    send_experts = torch.empty(S, dtype=torch.int64, device=dev)
+    send_scores = torch.empty(S, dtype=torch.float32, device=dev)
+    call("moe_dispatch_meta", ptr(ids), ptr(sc), ptr(perm), S, local_count, ptr(send_experts), ptr(send_scores), s)
+    source_tokens = torch.div(perm, k, rounding_mode="floor").to(torch.int64)
+    return send_hidden, send_experts, send_scores.to(scores.dtype), source_tokens, pos, counts
+
+
+@dispatch_fwd.register_fake
+def _(hidden, global_indices, scores, local_count, ep_size):
+    S = global_indices.shape[0] * global_indices.shape[1]
+    return (hidden.new_empty(S, hidden.shape[1]), global_indices.new_empty(S, dtype=torch.int64),
+            scores.new_empty(S), global_indices.new_empty(S, dtype=torch.int64),
+            global_indices.new_empty(S, dtype=torch.int32), global_indices.new_empty(ep_size, dtype=torch.int32))
+
+
+def _dispatch_setup(ctx, inputs, output):
+    hidden, global_indices, scores, local_count, ep_size = inputs
+    _, send_experts, _, source_tokens, pos, counts = output
+    ctx.save_for_backward(pos)
+    ctx.T, ctx.k = global_indices.shape
+    ctx.hidden_dtype = hidden.dtype
+    ctx.scores_dtype = scores.dtype
+    ctx.mark_non_differentiable(send_experts, source_tokens, pos, counts)
+
+
+def _dispatch_backward(ctx, d_send_hidden, _d_experts, d_send_scores, *_unused):
+    (pos,) = ctx.saved_tensors
+    d_hidden = d_scores = None
+    if d_send_hidden is not None:
+        d_hidden = combine_rows_fwd(d_send_hidden.to(BF16).contiguous(), pos, ctx.T, ctx.k).to(ctx.hidden_dtype)
+    if d_send_scores is not None:
+        d_scores = d_send_scores.index_select(0, pos.long()).view(ctx.T, ctx.k).to(ctx.scores_dtype)
+    return d_hidden, None, d_scores, None, None
+
+
+dispatch_fwd.register_autograd(_dispatch_backward, setup_context=_dispatch_setup)
+
+
+@torch.library.custom_op(f"{LIB}::combine_rows_fwd", mutates_args=())
+def combine_rows_fwd(rows: Tensor, pos_of_slot: Tensor, num_tokens: int, top_k: int) -> Tensor:
+    """out[t] = sum_j rows[pos_of_slot[t*k+j]] — TokenDispatcher.combine's index_add in gather form."""
+    _require_gpu(rows, pos_of_slot)
+    _require_bf16("combined rows", rows)
+    S, H = rows.shape
+    if S != num_tokens * top_k or pos_of_slot.numel() != S:
+        raise ValueError(f"combine expects {num_tokens}*{top_k} rows, got {S}")
+    out = torch.empty(num_tokens, H, dtype=rows.dtype, device=rows.device)
+    n_valid = torch.full((1,), S, dtype=torch.int32, device=rows.device)
+    call("moe_combine_fwd", ptr(rows.contiguous()), ptr(pos_of_slot), ptr(n_valid), 1, None, num_tokens, H, top_k,
+         ptr(out), _stream(rows))
+    return out
+
+
+@combine_rows_fwd.register_fake
+def _(rows, pos_of_slot, num_tokens, top_k):
+    return rows.new_empty(num_tokens, rows.shape[1])
+
+
+@torch.library.custom_op(f"{LIB}::combine_rows_bwd", mutates_args=())
+def combine_rows_bwd(d_out: Tensor, pos_of_slot: Tensor, top_k: int) -> Tensor:
+    """d_rows[pos_of_slot[t*k+j]] = d_out[t]."""
+    T, H = d_out.shape
+    S = T * top_k
+    d_rows = torch.empty(S, H, dtype=BF16, device=d_out.device)
+    n_valid = torch.full((1,), S, dtype=torch.int32, device=d_out.device)
+    call("moe_combine_bwd", ptr(d_out.to(BF16).contiguous()), None, ptr(pos_of_slot), ptr(n_valid), 1, None, T, H,
+         top_k, ptr(d_rows), None, _stream(d_out))
+    return d_rows
+
+
+@combine_rows_bwd.register_fake
+def _(d_out, pos_of_slot, top_k):
+    return d_out.new_empty(d_out.shape[0] * top_k, d_out.shape[1])
+
+
+def _combine_setup(ctx, inputs, output):
+    _, pos, _, top_k = inputs
+    ctx.save_for_backward(pos)
+    ctx.top_k = top_k
+
+
+def _combine_backward(ctx, d_out):
+    (pos,) = ctx.saved_tensors
+    return combine_rows_bwd(d_out, pos, ctx.top_k), None, None, None
+
+
+combine_rows_fwd.register_autograd(_combine_backward, setup_context=_combine_setup)

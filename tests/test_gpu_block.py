@@ -1,0 +1,208 @@
+"""Block-level parity on the GPU: router -> experts -> combine + aux loss,
+forward and backward, against the CPU oracle, the transformers golden
+vectors, and size-independent properties at the benchmark's full size."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, close_bf16
+from oracle import moe_oracle as O
+from parallel_amd import (
+    ExpertPartition,
+    SparseMoeBlock,
+    TokenDispatcher,
+    load_balancing_loss_func,
+    ops,
+    register_experts_implementation,
+)
+from parallel_amd.workloads import WORKLOADS, Workload, ep_receive_buffer, make_block_inputs, scaled
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def gpu_block_step(w: Workload, inp, logit_bias=None):
+    """Forward + backward of <out, d_out> + coef * aux on the gfx950 path."""
+    x = inp["x"].to(DEV).requires_grad_()
+    rw = inp["router_weight"].to(DEV).requires_grad_()
+    gu = inp["gate_up_proj"].to(DEV).requires_grad_()
+    dn = inp["down_proj"].to(DEV).requires_grad_()
+    bias = None if logit_bias is None else logit_bias.to(DEV)
+    logits, scores, idx = ops.router_fwd(x, rw, w.top_k, w.norm_topk_prob, bias)
+    out = ops.experts(x, idx, scores, gu, dn)
+    aux = load_balancing_loss_func((logits,), w.experts, w.top_k)
+    torch.autograd.backward([out, aux], [inp["d_out"].to(DEV), torch.tensor(w.aux_coef, device=DEV)])
+    return dict(logits=logits.detach(), scores=scores.detach(), indices=idx, out=out.detach(), aux=aux.detach(),
+                dx=x.grad, d_router=rw.grad, d_gate_up=gu.grad, d_down=dn.grad)
+
+
+def oracle_step(w, inp, logit_bias=None):
+    return O.block_forward_backward(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"],
+                                    inp["d_out"], top_k=w.top_k, norm_topk_prob=w.norm_topk_prob,
+                                    aux_coef=w.aux_coef, logit_bias=logit_bias)
+
+
+def compare(gpu, ref, tag):
+    ties = O.topk_ties(gpu["logits"].cpu(), ref["indices"])
+    routed = O.topk_softmax(gpu["logits"].cpu(), gpu["indices"].shape[1], True)[1]
+    assert not ((routed != gpu["indices"].cpu()).any(1) & ~ties).any(), f"{tag}: routing differs on the same logits"
+    assert not ((ref["indices"] != gpu["indices"].cpu()).any(1) & ~ties).any(), f"{tag}: routing differs"
+    close_bf16(gpu["logits"], ref["logits"], f"{tag} logits", max_rel=1e-4, min_cos=0.999999)
+    close_bf16(gpu["scores"], ref["scores"], f"{tag} scores", max_rel=1e-4, min_cos=0.999999)
+    torch.testing.assert_close(gpu["aux"].cpu(), ref["aux"], rtol=1e-4, atol=1e-6)
+    for key in ("out", "dx", "d_router", "d_gate_up", "d_down"):
+        close_bf16(gpu[key], ref[key], f"{tag} {key}")
+
+
+def test_block_c1_shape_against_oracle_and_transformers_golden():
+    w = WORKLOADS["c1"]
+    inp = make_block_inputs(w, seed=1234, dtype=BF)
+    gpu = gpu_block_step(w, inp)
+    compare(gpu, oracle_step(w, inp), "c1")
+    # transformers' own fp32 block on the unrounded inputs: same bar at bf16 precision
+    g = np.load(GOLDEN / "c1_qwen3_moe_block.npz")
+    for key in ("out", "dx", "d_router", "d_gate_up", "d_down"):
+        close_bf16(gpu[key], torch.from_numpy(g[key]), f"c1 golden {key}")
+
+
+@pytest.mark.parametrize("name,tokens", [("c2", 384), ("c5", 160)])
+def test_block_scaled_configs_against_oracle(name, tokens):
+    w = scaled(WORKLOADS[name], tokens)
+    inp = make_block_inputs(w, seed=5, dtype=BF)
+    compare(gpu_block_step(w, inp), oracle_step(w, inp), name)
+
+
+def test_block_c4_imbalanced_router_with_aux_gradient():
+    w = scaled(WORKLOADS["c4"], 512)
+    inp = make_block_inputs(w, seed=6, dtype=BF)
+    gpu = gpu_block_step(w, inp, inp["logit_bias"])
+    ref = oracle_step(w, inp, inp["logit_bias"])
+    compare(gpu, ref, "c4")
+    counts = torch.bincount(gpu["indices"].cpu().reshape(-1), minlength=w.experts)
+    assert counts.max() > 1.5 * counts.float().mean(), "the bias should skew the routing"
+
+
+def test_ep_share_receive_layout_c3():
+    w = scaled(WORKLOADS["c3"], 384)
+    _, _, (src, tok, lexp, lsc) = ep_receive_buffer(w, seed=3)
+    R = src.shape[0]
+    inp = make_block_inputs(w, seed=3, dtype=BF)
+    xs = [inp["x"], torch.randn(w.tokens, w.hidden, generator=torch.Generator().manual_seed(99)).to(BF)]
+    hidden = torch.stack([xs[s][t] for s, t in zip(src.tolist(), tok.tolist())])
+    idx = torch.from_numpy(lexp).view(R, 1)
+    sc = torch.from_numpy(lsc).view(R, 1)
+    assert (torch.bincount(idx.view(-1), minlength=64) == 0).sum() >= 4, "some local experts must be empty"
+    d_out = torch.randn(R, w.hidden, generator=torch.Generator().manual_seed(7)).to(BF)
+    h = hidden.to(DEV).requires_grad_()
+    s = sc.to(DEV).requires_grad_()
+    gu = inp["gate_up_proj"].to(DEV).requires_grad_()
+    dn = inp["down_proj"].to(DEV).requires_grad_()
+    out = ops.experts(h, idx.to(DEV), s, gu, dn)
+    out.backward(d_out.to(DEV))
+    hr = hidden.float().requires_grad_()
+    sr = sc.clone().requires_grad_()
+    gr = inp["gate_up_proj"].float().requires_grad_()
+    dr = inp["down_proj"].float().requires_grad_()
+    ref = O.experts_grouped(hr, idx, sr, gr, dr)
+    ref.backward(d_out.float())
+    close_bf16(out, ref, "c3 out")
+    close_bf16(h.grad, hr.grad, "c3 d_hidden")
+    close_bf16(s.grad, sr.grad, "c3 d_scores")
+    close_bf16(gu.grad, gr.grad, "c3 d_gate_up")
+    close_bf16(dn.grad, dr.grad, "c3 d_down")
+    empty = torch.bincount(idx.view(-1), minlength=64) == 0
+    assert not gu.grad[empty.to(DEV)].any() and not dn.grad[empty.to(DEV)].any()
+
+
+def test_sentinel_routes_match_transformers_golden():
+    w = WORKLOADS["c1"]
+    g = np.load(GOLDEN / "c1_qwen3_moe_block.npz")
+    inp = make_block_inputs(w, seed=1234, dtype=BF)
+    half = w.experts // 2
+    idx = torch.from_numpy(g["sentinel_local_idx"])
+    scores = torch.from_numpy(g["scores"]).masked_fill(idx == half, 0)
+    out = ops.experts(inp["x"].to(DEV), idx.to(DEV), scores.to(DEV), inp["gate_up_proj"][:half].to(DEV),
+                      inp["down_proj"][:half].to(DEV))
+    close_bf16(out, torch.from_numpy(g["sentinel_out"]), "sentinel out")
+
+
+def test_token_dispatcher_round_trip_closed_form():
+    # One-rank analogue of parallel tests/test_sequence_parallel.py:17-73.
+    T, H, k, E = 64, 32, 2, 4
+    hidden = torch.randn(T, H, generator=torch.Generator().manual_seed(1)).to(BF).to(DEV).requires_grad_()
+    raw = torch.rand(T, k, generator=torch.Generator().manual_seed(2))
+    scores = (raw / raw.sum(1, keepdim=True)).to(DEV).requires_grad_()
+    indices = torch.stack([torch.randperm(E, generator=torch.Generator().manual_seed(t))[:k] for t in range(T)])
+    dispatcher = TokenDispatcher(ExpertPartition(E, 1, 0), None)
+    received, local_idx, rscores, state = dispatcher.dispatch(hidden, indices.to(DEV), scores)
+    assert state.send_splits == (T * k,) and received.shape == (T * k, H)
+    ref_h, ref_e, ref_s, ref_src, _ = O.dispatch_send(hidden.detach().cpu(), indices, scores.detach().cpu(), E, 1)
+    assert torch.equal(received.detach().cpu(), ref_h) and torch.equal(local_idx.cpu().view(-1), ref_e)
+    assert torch.equal(state.source_tokens.cpu(), ref_src)
+    combined = dispatcher.combine(received * rscores.to(received.dtype), state)
+    close_bf16(combined, hidden.detach(), "round trip", max_rel=1e-2)
+    combined.float().square().sum().backward()
+    close_bf16(hidden.grad, 2 * combined.detach(), "d_hidden", max_rel=2e-2)
+    ref_ds = 2 * (hidden.detach().float() * combined.detach().float()).sum(-1, keepdim=True).expand(T, k)
+    close_bf16(scores.grad, ref_ds, "d_scores", max_rel=2e-2)
+
+
+def test_transformers_block_runs_on_the_plugin():
+    from transformers import Qwen3MoeConfig
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeSparseMoeBlock
+
+    assert register_experts_implementation()
+    cfg = Qwen3MoeConfig(hidden_size=256, num_experts=8, num_experts_per_tok=2, moe_intermediate_size=128,
+                         norm_topk_prob=True)
+    cfg._experts_implementation = "mi355x"
+    torch.manual_seed(0)
+    block = Qwen3MoeSparseMoeBlock(cfg)
+    with torch.no_grad():
+        for p in block.parameters():
+            p.normal_(0, 0.05)
+    ref_block = Qwen3MoeSparseMoeBlock(cfg)
+    ref_block.load_state_dict(block.state_dict())
+    ref_block.config._experts_implementation = "eager"
+    block = block.to(DEV, BF)
+    x = torch.randn(2, 64, 256)
+    xg = x.to(DEV, BF).requires_grad_()
+    _, sc, ix = block.gate(xg.view(-1, 256))
+    out = block.experts(xg.view(-1, 256), ix, sc)
+    ref = O.experts_eager(x.to(BF).float().view(-1, 256), ix.cpu(), sc.detach().cpu().float(),
+                          ref_block.experts.gate_up_proj.detach().to(BF).float(),
+                          ref_block.experts.down_proj.detach().to(BF).float())
+    close_bf16(out, ref, "transformers plugin out")
+    out.float().square().sum().backward()
+    assert block.experts.gate_up_proj.grad is not None and torch.isfinite(xg.grad.float()).all()
+
+
+def test_full_c2_forward_properties_and_sampled_tokens():
+    w = WORKLOADS["c2"]
+    inp = make_block_inputs(w, seed=11, device=DEV, dtype=BF, weights_on_device_rng=True)
+    x = inp["x"]
+    logits, scores, idx = ops.router_fwd(x, inp["router_weight"], w.top_k, True)
+    gu, dn = inp["gate_up_proj"], inp["down_proj"]
+    out1, xp, pre, act, y, pos, offsets = ops.experts_fwd(x, idx, scores, gu, dn)
+    out2 = ops.experts_fwd(x, idx, scores, gu, dn)[0]
+    assert torch.equal(out1, out2), "forward must be deterministic"
+    # permutation invariants at full size
+    off = offsets.cpu().long()
+    assert int(off[-1]) == w.slots and bool((off[1:] >= off[:-1]).all())
+    p = pos.cpu().long()
+    assert torch.equal(torch.sort(p).values, torch.arange(w.slots))
+    ids_sorted = idx.cpu().reshape(-1)[torch.argsort(p)]
+    assert bool((ids_sorted[1:] >= ids_sorted[:-1]).all())
+    # linearity: doubling the activations doubles the up-projection exactly
+    act2 = torch.empty_like(act)
+    pre2 = torch.empty_like(pre)
+    from parallel_amd import _lib
+    xp2 = xp * 2
+    _lib.call("moe_grouped_gemm_swiglu_fwd", xp2.data_ptr(), gu.data_ptr(), offsets.data_ptr(), w.experts, w.slots,
+              w.hidden, w.intermediate, act2.data_ptr(), pre2.data_ptr(), _lib.stream_of(xp2))
+    assert torch.equal(pre2, pre * 2)
+    # sampled tokens against the oracle (the forward is per-token independent)
+    sample = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(0))[:48]
+    ref = O.experts_grouped(x.cpu()[sample], idx.cpu()[sample], scores.cpu()[sample], gu.cpu(), dn.cpu())
+    close_bf16(out1.cpu()[sample], ref, "c2 sampled tokens")

@@ -1,0 +1,347 @@
+"""Per-kernel parity on the GPU, through the C-ABI ops, against the CPU oracle
+(integers bit-exact) and plain fp32 torch references (floating point)."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import close_bf16
+from oracle import moe_oracle as O
+from parallel_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ------------------------------------------------------------------- router
+
+ROUTER_CASES = [(512, 8, 2, True), (4096, 128, 8, True), (1000, 128, 8, False), (257, 64, 4, True),
+                (64, 1024, 16, True), (33, 3, 3, False)]
+
+
+@pytest.mark.parametrize("T,E,k,norm", ROUTER_CASES)
+def test_router_topk_bit_exact_on_same_logits(T, E, k, norm):
+    logits = torch.randn(T, E, generator=gen(T + E))
+    scores, idx = ops.router_topk(logits.to(DEV), k, norm)
+    ref_scores, ref_idx = O.topk_softmax(logits, k, norm)
+    ties = O.topk_ties(logits, ref_idx)
+    mismatch = (idx.cpu() != ref_idx).any(dim=1)
+    assert not (mismatch & ~ties).any(), f"{int((mismatch & ~ties).sum())} tokens routed differently"
+    ok = ~ties
+    torch.testing.assert_close(scores.cpu()[ok], ref_scores[ok], rtol=2e-6, atol=1e-7)
+
+
+def test_router_topk_ties_go_to_lower_index():
+    logits = torch.zeros(4, 16)
+    logits[1, 5] = 1.0
+    scores, idx = ops.router_topk(logits.to(DEV), 4, False)
+    assert idx[0].tolist() == [0, 1, 2, 3]
+    assert idx[1].tolist() == [5, 0, 1, 2]
+    torch.testing.assert_close(scores[0].cpu(), torch.full((4,), 1 / 16))
+
+
+@pytest.mark.parametrize("T,H,E", [(512, 256, 8), (4096, 2048, 128), (300, 72, 24)])
+def test_router_logits_match_fp32(T, H, E):
+    x = torch.randn(T, H, generator=gen(1)).to(BF)
+    w = (torch.randn(E, H, generator=gen(2)) * 0.02).to(BF)
+    logits, scores, idx = ops.router_fwd(x.to(DEV), w.to(DEV), min(8, E), True)
+    ref = O.router_logits(x, w)
+    torch.testing.assert_close(logits.cpu(), ref, rtol=1e-4, atol=1e-5)
+    ref_s, ref_i = O.topk_softmax(logits.cpu(), min(8, E), True)
+    ties = O.topk_ties(logits.cpu(), ref_i)
+    assert not ((idx.cpu() != ref_i).any(1) & ~ties).any()
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_backward_matches_autograd(norm):
+    T, H, E, k = 384, 256, 16, 4
+    x = torch.randn(T, H, generator=gen(3)).to(BF)
+    w = (torch.randn(E, H, generator=gen(4)) * 0.05).to(BF)
+    d_scores = torch.randn(T, k, generator=gen(5))
+    d_logits = torch.randn(T, E, generator=gen(6)) * 0.01
+    xg = x.to(DEV).requires_grad_()
+    wg = w.to(DEV).requires_grad_()
+    logits, scores, idx = ops.router_fwd(xg, wg, k, norm)
+    torch.autograd.backward([scores, logits], [d_scores.to(DEV), d_logits.to(DEV)])
+    xr = x.float().requires_grad_()
+    wr = w.float().requires_grad_()
+    lr = O.router_logits(xr, wr)
+    sr, ir = O.topk_softmax(lr, k, norm)
+    assert torch.equal(ir, idx.cpu())
+    torch.autograd.backward([sr, lr], [d_scores, d_logits])
+    close_bf16(xg.grad, xr.grad, "router dx")
+    close_bf16(wg.grad, wr.grad, "router dweight")
+
+
+# ------------------------------------------------------------------ aux loss
+
+
+@pytest.mark.parametrize("T,E,k,masked", [(512, 8, 2, False), (4096, 128, 8, False), (2 * 96, 64, 6, True)])
+def test_aux_loss_forward_backward(T, E, k, masked):
+    logits = torch.randn(T, E, generator=gen(T)) * 2
+    mask = None
+    if masked:
+        mask = (torch.rand(2, T // 2, generator=gen(9)) > 0.3).float()
+    lg = logits.to(DEV).requires_grad_()
+    tw = None if mask is None else mask.reshape(-1).to(DEV)
+    aux, stats = ops.aux_loss_fwd(lg, tw, E, k)
+    aux.backward(torch.tensor(0.7, device=DEV))
+    lr = logits.clone().requires_grad_()
+    ref = O.load_balancing_loss((lr,), E, k, attention_mask=mask)
+    (0.7 * ref).backward()
+    torch.testing.assert_close(aux.cpu(), ref.detach(), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(lg.grad.cpu(), lr.grad, rtol=1e-4, atol=1e-8)
+
+
+def test_aux_loss_balanced_routing_is_top_k():
+    E, k, T = 8, 2, 64
+    logits = torch.randn(T, E, generator=gen(0)) * 0.1
+    for t in range(T):
+        logits[t, (2 * t) % E] += 5.0
+        logits[t, (2 * t + 1) % E] += 4.0
+    aux, stats = ops.aux_loss_fwd(logits.to(DEV), None, E, k)
+    assert abs(float(aux) - k) < 1e-5
+    assert stats.cpu().tolist() == [16.0] * E + [64.0]
+
+
+# ------------------------------------------------------------------- permute
+
+
+def _perm_case(T, k, E, seed, sentinel_frac=0.0, skew=None, distinct=True):
+    g = gen(seed)
+    if distinct and k <= E:
+        keys = torch.rand(T, E, generator=g)
+        if skew is not None:
+            keys = keys + skew
+        ids = keys.topk(k, dim=1).indices
+    else:
+        ids = torch.randint(0, E, (T, k), generator=g)
+    if sentinel_frac:
+        ids = ids.masked_fill(torch.rand(T, k, generator=g) < sentinel_frac, E)
+    return ids
+
+
+PERMUTE_CASES = [
+    dict(T=4096, k=8, E=128, seed=1),
+    dict(T=16384, k=8, E=128, seed=2, skew=torch.linspace(0, 2, 128)),
+    dict(T=512, k=2, E=8, seed=3),
+    dict(T=1, k=1, E=4, seed=4),
+    dict(T=3000, k=4, E=64, seed=5, sentinel_frac=0.4),
+    dict(T=700, k=3, E=1024, seed=6, distinct=False),
+    dict(T=2049, k=1, E=2, seed=7, distinct=False),
+]
+
+
+@pytest.mark.parametrize("case", PERMUTE_CASES, ids=lambda c: f"T{c['T']}k{c['k']}E{c['E']}")
+def test_permute_bit_exact(case):
+    case = dict(case)
+    T, k, E = case["T"], case["k"], case["E"]
+    ids = _perm_case(**case)
+    H = 64
+    hidden = torch.randn(T, H, generator=gen(11)).to(BF)
+    rows, perm, pos, counts, offsets = ops.permute_fwd(hidden.to(DEV), ids.to(DEV), 1, E, True)
+    r_perm, r_pos, r_counts, r_off = O.stable_permutation(ids.numpy(), 1, E)
+    assert np.array_equal(perm.cpu().numpy(), r_perm)
+    assert np.array_equal(pos.cpu().numpy(), r_pos)
+    assert np.array_equal(counts.cpu().numpy(), r_counts)
+    assert np.array_equal(offsets.cpu().numpy(), r_off)
+    n_valid = int(r_off[-1])
+    expect = hidden[torch.from_numpy(r_perm[:n_valid]) // k]
+    assert torch.equal(rows.cpu()[:n_valid], expect), "gathered rows are not exact copies"
+    assert not rows.cpu()[n_valid:].any(), "sentinel rows must be zero"
+
+
+def test_permute_matches_torch_sort_histc_cumsum():
+    ids = _perm_case(4096, 8, 128, 21)
+    _, perm, _, counts, offsets = ops.permute_fwd(torch.empty(4096, 8, dtype=BF, device=DEV), ids.to(DEV), 1, 128,
+                                                  False)
+    flat = ids.reshape(-1)
+    _, ref_perm = torch.sort(flat, stable=True)
+    hist = torch.histc(flat.float(), bins=128, min=0, max=127)
+    assert torch.equal(perm.cpu().long(), ref_perm)
+    assert torch.equal(counts.cpu().long(), torch.bincount(flat, minlength=128))
+    assert torch.equal(offsets.cpu(), torch.cumsum(hist, 0, dtype=torch.int32))
+
+
+def test_permute_owner_buckets_give_send_splits():
+    ids = _perm_case(2048, 8, 128, 22)
+    _, perm, _, counts, _ = ops.permute_fwd(torch.empty(2048, 8, dtype=BF, device=DEV), ids.to(DEV), 16, 8, False)
+    dest = ids.reshape(-1) // 16
+    assert torch.equal(perm.cpu().long(), torch.argsort(dest, stable=True))
+    assert torch.equal(counts.cpu().long(), torch.bincount(dest, minlength=8))
+
+
+def test_permute_empty_input():
+    _, perm, pos, counts, offsets = ops.permute_fwd(torch.empty(0, 64, dtype=BF, device=DEV),
+                                                    torch.empty(0, 8, dtype=torch.long, device=DEV), 1, 16, True)
+    assert perm.numel() == 0 and counts.cpu().tolist() == [0] * 16 and offsets.cpu().tolist() == [0] * 16
+
+
+# -------------------------------------------------------------- grouped GEMM
+
+
+def _groups(counts):
+    counts = torch.tensor(counts, dtype=torch.int64)
+    return counts, torch.cumsum(counts, 0).to(torch.int32)
+
+
+def _ref_fwd(a, w, counts):
+    out, s = [], 0
+    for e, c in enumerate(counts.tolist()):
+        out.append(a[s:s + c].float() @ w[e].float().t())
+        s += c
+    return torch.cat(out)
+
+
+GEMM_CASES = [
+    ("c2like", [256, 0, 300, 1, 128, 255, 513], 1536, 2048),
+    ("ragged", [7, 0, 0, 130, 64, 1], 200, 72),
+    ("single", [1000], 128, 256),
+]
+
+
+@pytest.mark.parametrize("name,cnt,N,K", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+def test_grouped_gemm_fwd(name, cnt, N, K):
+    counts, offs = _groups(cnt)
+    M = int(counts.sum()) + 5  # trailing rows past offs[-1] are not touched
+    G = len(cnt)
+    a = torch.randn(M, K, generator=gen(1)).to(BF)
+    w = (torch.randn(G, N, K, generator=gen(2)) * 0.05).to(BF)
+    c = torch.full((M, N), 7.0, dtype=BF, device=DEV)
+    _lib.call("moe_grouped_gemm_fwd", a.to(DEV).data_ptr(), (wd := w.to(DEV)).data_ptr(),
+              (od := offs.to(DEV)).data_ptr(), G, M, N, K, c.data_ptr(), _lib.stream_of(c))
+    torch.cuda.synchronize()
+    n = int(counts.sum())
+    close_bf16(c[:n], _ref_fwd(a, w, counts), f"fwd {name}", max_rel=8e-3)
+    assert (c[n:].float() == 7.0).all(), "rows past offs[-1] were written"
+
+
+@pytest.mark.parametrize("name,cnt,N,K", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+def test_grouped_gemm_dgrad(name, cnt, N, K):
+    counts, offs = _groups(cnt)
+    M = int(counts.sum())
+    G = len(cnt)
+    dc = torch.randn(M, N, generator=gen(3)).to(BF)
+    w = (torch.randn(G, N, K, generator=gen(4)) * 0.05).to(BF)
+    da = torch.empty(M, K, dtype=BF, device=DEV)
+    _lib.call("moe_grouped_gemm_dgrad", (dcd := dc.to(DEV)).data_ptr(), (wd := w.to(DEV)).data_ptr(),
+              (od := offs.to(DEV)).data_ptr(), G, M, N, K, da.data_ptr(), _lib.stream_of(da))
+    ref, s = [], 0
+    for e, c in enumerate(counts.tolist()):
+        ref.append(dc[s:s + c].float() @ w[e].float())
+        s += c
+    close_bf16(da, torch.cat(ref), f"dgrad {name}", max_rel=8e-3)
+
+
+@pytest.mark.parametrize("name,cnt,N,K", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+@pytest.mark.parametrize("accumulate,f32", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_grouped_gemm_wgrad(name, cnt, N, K, accumulate, f32):
+    counts, offs = _groups(cnt)
+    M = int(counts.sum())
+    G = len(cnt)
+    dc = torch.randn(M, N, generator=gen(5)).to(BF)
+    a = torch.randn(M, K, generator=gen(6)).to(BF)
+    base = torch.randn(G, N, K, generator=gen(7))
+    dw = base.to(torch.float32 if f32 else BF).to(DEV)
+    _lib.call("moe_grouped_gemm_wgrad", (dcd := dc.to(DEV)).data_ptr(), (ad := a.to(DEV)).data_ptr(),
+              (od := offs.to(DEV)).data_ptr(), G, M, N, K, dw.data_ptr(), f32, accumulate, _lib.stream_of(dw))
+    s = 0
+    start = base.to(torch.float32 if f32 else BF).float()
+    for e, c in enumerate(counts.tolist()):
+        ref = dc[s:s + c].float().t() @ a[s:s + c].float()
+        if accumulate:
+            ref = ref + start[e]
+        s += c
+        if c == 0 and accumulate:
+            assert torch.equal(dw[e].cpu().float(), start[e]), "accumulate must leave empty groups untouched"
+        elif c == 0:
+            assert not dw[e].cpu().float().any(), "empty group must get a zero gradient"
+        else:
+            close_bf16(dw[e], ref, f"wgrad {name} g{e}", max_rel=8e-3)
+
+
+@pytest.mark.parametrize("cnt,I,H", [([256, 0, 300, 1, 128], 768, 2048), ([5, 64, 0, 17], 64, 96)])
+def test_swiglu_fwd_and_fused_backward(cnt, I, H):
+    counts, offs = _groups(cnt)
+    M = int(counts.sum())
+    G = len(cnt)
+    xp = torch.randn(M, H, generator=gen(8)).to(BF)
+    gu = (torch.randn(G, 2 * I, H, generator=gen(9)) * 0.05).to(BF)
+    dn = (torch.randn(G, H, I, generator=gen(10)) * 0.05).to(BF)
+    dy = torch.randn(M, H, generator=gen(11)).to(BF)
+    act = torch.empty(M, I, dtype=BF, device=DEV)
+    pre = torch.empty(M, 2 * I, dtype=BF, device=DEV)
+    od = offs.to(DEV)
+    xpd, gud, dnd, dyd = xp.to(DEV), gu.to(DEV), dn.to(DEV), dy.to(DEV)
+    s = _lib.stream_of(act)
+    _lib.call("moe_grouped_gemm_swiglu_fwd", xpd.data_ptr(), gud.data_ptr(), od.data_ptr(), G, M, H, I,
+              act.data_ptr(), pre.data_ptr(), s)
+    ref_pre = _ref_fwd(xp, gu, counts)
+    gate, up = ref_pre.chunk(2, dim=-1)
+    close_bf16(pre, ref_pre, "swiglu pre", max_rel=8e-3)
+    close_bf16(act, F.silu(gate) * up, "swiglu act", max_rel=8e-3)
+    d_pre = torch.empty(M, 2 * I, dtype=BF, device=DEV)
+    _lib.call("moe_grouped_gemm_dgrad_swiglu_bwd", dyd.data_ptr(), dnd.data_ptr(), pre.data_ptr(), od.data_ptr(),
+              G, M, H, I, d_pre.data_ptr(), s)
+    # reference: autograd of silu(g)*u at the saved (bf16) pre-activation
+    p = pre.cpu().float().requires_grad_()
+    g2, u2 = p.chunk(2, dim=-1)
+    d_act, s0 = [], 0
+    for e, c in enumerate(counts.tolist()):
+        d_act.append(dy[s0:s0 + c].float() @ dn[e].float())
+        s0 += c
+    (F.silu(g2) * u2).backward(torch.cat(d_act))
+    close_bf16(d_pre, p.grad, "swiglu d_pre", max_rel=1e-2)
+
+
+# ------------------------------------------------------------------- combine
+
+
+@pytest.mark.parametrize("T,k,E,H,sent", [(512, 2, 8, 256, 0.0), (1024, 8, 128, 2048, 0.0), (300, 4, 16, 72, 0.3)])
+def test_combine_forward_backward(T, k, E, H, sent):
+    ids = _perm_case(T, k, E, 31, sentinel_frac=sent)
+    hidden = torch.randn(T, H, generator=gen(32)).to(BF)
+    rows, perm, pos, counts, offsets = ops.permute_fwd(hidden.to(DEV), ids.to(DEV), 1, E, True)
+    S = T * k
+    y = torch.randn(S, H, generator=gen(33)).to(BF)
+    scores = torch.rand(T, k, generator=gen(34))
+    out = torch.empty(T, H, dtype=BF, device=DEV)
+    yd, sd = y.to(DEV), scores.to(DEV)
+    st = _lib.stream_of(out)
+    _lib.call("moe_combine_fwd", yd.data_ptr(), pos.data_ptr(), offsets.data_ptr(), E, sd.data_ptr(), T, H, k,
+              out.data_ptr(), st)
+    posc = pos.cpu().long().view(T, k)
+    valid = ids < E
+    ref = (y.float()[posc] * (scores * valid).unsqueeze(-1)).sum(1)
+    close_bf16(out, ref, "combine fwd", max_rel=8e-3)
+    d_out = torch.randn(T, H, generator=gen(35)).to(BF)
+    dy = torch.full((S, H), 3.0, dtype=BF, device=DEV)
+    d_s = torch.empty(T * k, dtype=torch.float32, device=DEV)
+    _lib.call("moe_combine_bwd", (dd := d_out.to(DEV)).data_ptr(), yd.data_ptr(), pos.data_ptr(),
+              offsets.data_ptr(), E, sd.data_ptr(), T, H, k, dy.data_ptr(), d_s.data_ptr(), st)
+    ref_dy = torch.zeros(S, H)
+    ref_dy[posc.reshape(-1)] = (d_out.float().unsqueeze(1) * (scores * valid).unsqueeze(-1)).reshape(S, H)
+    close_bf16(dy, ref_dy, "combine d_y", max_rel=8e-3)
+    ref_ds = (y.float()[posc] * d_out.float().unsqueeze(1)).sum(-1) * valid
+    close_bf16(d_s.view(T, k), ref_ds, "combine d_scores", max_rel=1e-3)
+
+
+def test_permute_backward_sums_routes():
+    T, k, E, H = 777, 4, 32, 136
+    ids = _perm_case(T, k, E, 41, sentinel_frac=0.2)
+    hidden = torch.zeros(T, H, dtype=BF, device=DEV)
+    _, perm, pos, counts, offsets = ops.permute_fwd(hidden, ids.to(DEV), 1, E, False)
+    dperm = torch.randn(T * k, H, generator=gen(42)).to(BF)
+    d_add = torch.randn(T, H, generator=gen(43)).to(BF)
+    dh = torch.empty(T, H, dtype=BF, device=DEV)
+    _lib.call("moe_permute_bwd", (dp := dperm.to(DEV)).data_ptr(), pos.data_ptr(), offsets.data_ptr(), E, T, H, k,
+              (da := d_add.to(DEV)).data_ptr(), dh.data_ptr(), _lib.stream_of(dh))
+    posc = pos.cpu().long().view(T, k)
+    ref = (dperm.float()[posc] * (ids < E).unsqueeze(-1)).sum(1) + d_add.float()
+    close_bf16(dh, ref, "permute bwd", max_rel=8e-3)

@@ -1,0 +1,115 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every
+declared symbol, argument validation raises the reference's exception types,
+and there is no CPU fallback."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+from parallel_amd import (
+    ExpertPartition,
+    TokenDispatcher,
+    load_balancing_loss_func,
+    register_experts_implementation,
+    sequence_parallel_load_balancing_loss,
+)
+from parallel_amd import _lib, ops
+from parallel_amd.workloads import WORKLOADS
+
+HEADER = ROOT / "include" / "moe_mi355x.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    assert len(syms) >= 18
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH}"
+    assert lib.moe_abi_version() == _lib.ABI_VERSION
+
+
+def test_library_size_queries_and_argument_checks_run_without_a_gpu():
+    lib = _lib.load()
+    assert lib.moe_permute_workspace_bytes(32768, 128) == 16 * 129 * 4
+    assert lib.moe_aux_loss_workspace_bytes(4096, 128) == 64 * 257 * 4
+    # invalid sizes are rejected before any HIP call
+    rc = lib.moe_grouped_gemm_fwd(None, None, None, 1, 8, 8, 8, None, None)
+    assert rc == _lib.MOE_ERR_INVALID
+    assert b"null" in lib.moe_last_error()
+    buf = ctypes.create_string_buffer(64)
+    rc = lib.moe_grouped_gemm_fwd(ctypes.addressof(buf), ctypes.addressof(buf), None, 1, 8, 12, 8, None, None)
+    assert rc in (_lib.MOE_ERR_UNSUPPORTED, _lib.MOE_ERR_INVALID)
+    with pytest.raises(ValueError, match="top_k"):
+        _lib.check(lib.moe_router_topk_fwd(None, None, None, 4, 8, 9, 1, None), "topk")
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.randn(4, 16, dtype=torch.bfloat16)
+    w = torch.randn(8, 16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.router_fwd(x, w, 2, True)
+    gu = torch.randn(8, 32, 16, dtype=torch.bfloat16)
+    dn = torch.randn(8, 16, 16, dtype=torch.bfloat16)
+    idx = torch.zeros(4, 2, dtype=torch.int64)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.experts(x, idx, torch.rand(4, 2), gu, dn)
+
+
+def test_expert_partition_contract():
+    with pytest.raises(ValueError, match="ep_size must be positive"):
+        ExpertPartition(8, 0, 0)
+    with pytest.raises(ValueError, match="outside the expert-parallel group"):
+        ExpertPartition(8, 2, 2)
+    with pytest.raises(ValueError, match="divisible"):
+        ExpertPartition(6, 4, 0)
+    p = ExpertPartition(num_experts=8, ep_size=2, ep_rank=1)
+    assert (p.local_count, p.start, p.stop, p.global_experts) == (4, 4, 8, range(4, 8))
+    # parallel tests/test_model_parallel.py:140-147
+    li, ls, m = p.localize_routes(torch.tensor([[0, 6], [4, 3]]), torch.tensor([[0.2, 0.8], [0.7, 0.3]]))
+    torch.testing.assert_close(li, torch.tensor([[4, 2], [0, 4]]))
+    torch.testing.assert_close(ls, torch.tensor([[0.0, 0.8], [0.7, 0.0]]))
+    torch.testing.assert_close(m, torch.tensor([[False, True], [True, False]]))
+    with pytest.raises(ValueError, match="same shape"):
+        p.localize_routes(torch.zeros(2, 2, dtype=torch.long), torch.zeros(2, 3))
+
+
+def test_token_dispatcher_contract():
+    with pytest.raises(ValueError, match="ep_size"):
+        TokenDispatcher(ExpertPartition(8, 2, 0), None)
+    d = TokenDispatcher(ExpertPartition(8, 1, 0), None)
+    with pytest.raises(ValueError, match="same shape"):
+        d.dispatch(torch.zeros(2, 8), torch.zeros(2, 2, dtype=torch.long), torch.zeros(2, 3))
+
+
+def test_aux_loss_api_edges():
+    assert load_balancing_loss_func(None, 8, 2) == 0
+    assert load_balancing_loss_func(torch.zeros(4, 8), 8, 2) == 0  # not a tuple: transformers returns 0
+    assert sequence_parallel_load_balancing_loss(None, num_experts=8, top_k=2, group=None) is None
+
+
+def test_transformers_registry_plugin():
+    assert register_experts_implementation()
+    from transformers.integrations.moe import ALL_EXPERTS_FUNCTIONS
+
+    assert "mi355x" in ALL_EXPERTS_FUNCTIONS
+
+
+def test_workload_shapes():
+    c2 = WORKLOADS["c2"]
+    assert (c2.tokens, c2.slots, c2.hidden, c2.experts, c2.top_k, c2.intermediate) == (4096, 32768, 2048, 128, 8, 768)
+    assert c2.gemm_flops() == pytest.approx(9.277e11, rel=1e-3)
+    assert WORKLOADS["c4"].gemm_flops() == pytest.approx(3.711e12, rel=1e-3)
+    assert WORKLOADS["c5"].gemm_flops() == pytest.approx(7.422e12, rel=1e-3)
