@@ -44,15 +44,13 @@ def kernel_work(w, T: int, S: int):
         "down_wgrad": ("mfma", 2.0 * S * H * I),
         "up_dgrad": ("mfma", 4.0 * S * H * I),
         "up_wgrad": ("mfma", 4.0 * S * H * I),
-        "router_logits": ("mfma", 2.0 * T * H * E),
-        "router_dgrad": ("mfma", 2.0 * T * H * E),
-        "router_wgrad": ("mfma", 2.0 * T * H * E),
+        "router_fwd": ("mfma", 2.0 * T * H * E),
+        "router_gemm_bwd": ("mfma", 4.0 * T * H * E),
         # bytes: read x rows once per route and ids, write permuted rows and maps
         "permute_fwd": ("hbm", T * H * b + S * H * b + 16.0 * S),
         "combine_fwd": ("hbm", S * H * b + 8.0 * S + T * H * b),
         "combine_bwd": ("hbm", T * H * b + 2.0 * S * H * b + 12.0 * S),
         "permute_bwd": ("hbm", S * H * b + T * H * b + 4.0 * S),
-        "router_topk": ("hbm", 4.0 * T * E + 12.0 * T * k),
         "router_topk_bwd": ("hbm", 8.0 * T * E + 2.0 * T * E + 16.0 * T * k),
         "aux_fwd": ("hbm", 4.0 * T * E),
         "aux_bwd": ("hbm", 8.0 * T * E),

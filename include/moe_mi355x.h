@@ -54,6 +54,18 @@ int moe_abi_version(void);
 int moe_router_logits_fwd(const void* x, const void* wr, float* logits,
                           int64_t T, int64_t H, int64_t E, void* stream);
 
+/* Fused router forward: logits = x · wrᵀ (+ logit_bias[E] when not NULL, f32),
+ * then the top-k softmax of moe_router_topk_fwd.  The GEMM is split along H
+ * into f32 partials held in the workspace, and one kernel reduces them and
+ * selects the top-k per token.  Replaces Qwen3MoeTopKRouter.forward
+ * (TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267); the reference router
+ * has no bias (the imbalanced benchmark configuration adds one). */
+size_t moe_router_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
+int moe_router_fwd(const void* x, const void* wr, const float* logit_bias,
+                   float* logits, float* scores, int64_t* indices, int64_t T,
+                   int64_t H, int64_t E, int64_t k, int norm_topk_prob,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* Per token: p = softmax(logits) in fp32; indices = the k largest, sorted
  * descending (ties: lower expert index first); scores = p[indices],
  * divided by their sum when norm_topk_prob != 0.
@@ -71,6 +83,15 @@ int moe_router_topk_bwd(const float* logits, const int64_t* indices,
                         const float* d_scores, int64_t T, int64_t E, int64_t k,
                         int norm_topk_prob, float* d_logits, int accumulate,
                         void* d_logits_bf16, void* stream);
+
+/* Backward of the router GEMM (F.linear, modeling_qwen3_moe.py:260) from
+ * bf16 d_logits[T,E]: dx[T,H] = d_logits · wr (bf16) and dwr[E,H] =
+ * d_logitsᵀ · x (bf16, reduced in f32 over row chunks held in the workspace). */
+size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
+int moe_router_logits_bwd(const void* d_logits_bf16, const void* x,
+                          const void* wr, void* dx, void* dwr, int64_t T,
+                          int64_t H, int64_t E, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- aux loss */
 

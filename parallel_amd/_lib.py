@@ -35,6 +35,10 @@ SIGNATURES: dict[str, tuple] = {
     "moe_last_error": (ctypes.c_char_p, []),
     "moe_abi_version": (_I, []),
     "moe_router_logits_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "moe_router_fwd_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "moe_router_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "moe_router_logits_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "moe_router_logits_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "moe_router_topk_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "moe_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _I, _P, _P]),
     "moe_aux_loss_workspace_bytes": (_SZ, [_I64, _I64]),

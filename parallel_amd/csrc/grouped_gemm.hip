@@ -23,7 +23,7 @@
 // happens in that XCD's L2.
 #include <stdarg.h>
 
-#include "common.h"
+#include "gemm.h"
 
 namespace moe {
 
@@ -45,9 +45,14 @@ struct GemmParams {
   int M, N, K;  // GEMM-internal sizes: MG: M = rows, N out cols, K reduction; KG: M x N output per group
   int64_t lda, ldb, ldc, ldp;
   int64_t stride_bg, stride_cg;
+  uint32_t a_bytes;  // bytes addressable through the A buffer resource
+  uint32_t b_bytes;  // bytes of one group's B (MG) or of all of B (KG)
   int swiglu_I;  // SWIGLU_FWD: intermediate size I (weight rows gate: [0,I), up: [I,2I))
   int accumulate;
   int n_tiles, m_tiles_max, total_blocks;
+  int k_splits, k_chunk;   // MG without groups: split the reduction, partial outputs stacked
+  int64_t split_stride;    // elements between split partials of C
+  int chunk_rows;          // KG without offs and G > 1: group g = rows [g*chunk_rows, ...)
 };
 
 // ---------------------------------------------------------------- helpers
@@ -81,9 +86,19 @@ __device__ __forceinline__ uint2 column4(const uint4 (&v)[4], int c) {
   return r;
 }
 
-__device__ __forceinline__ uint4 ldg16(const bf16_t* p, bool valid) {
-  uint4 z = make_uint4(0, 0, 0, 0);
-  return valid ? *reinterpret_cast<const uint4*>(p) : z;
+// Raw buffer loads: offsets at or past the resource's byte size read as zero
+// in hardware, so out-of-range rows and the K tail need no branches.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;  // >= every resource size (host checks < 2 GiB)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y), static_cast<uint32_t>(v.z),
+                    static_cast<uint32_t>(v.w));
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
@@ -151,6 +166,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   // ------------------------------------------------------ tile -> work
   int g, m0, n0;             // group, first output row (within group for KG), first output col
   int row_begin, row_end;    // MG: absolute activation rows of the group; KG: reduction rows
+  int split = 0, k_begin = 0;  // split-K partial index and its first reduction index
   const bf16_t* Bg = p.B;
   if constexpr (MODE == MODE_MG) {
     if (p.offs) {
@@ -166,14 +182,18 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       n0 = nt * BN;
     } else {
       int mtiles = (p.M + BM - 1) / BM;
-      if (L >= mtiles * p.n_tiles) return;
+      int per_split = mtiles * p.n_tiles;
+      split = L / per_split;
+      if (split >= p.k_splits) return;
+      int local = L - split * per_split;
       g = 0;
-      int nt = L / mtiles;
-      int mt = L - nt * mtiles;
+      int nt = local / mtiles;
+      int mt = local - nt * mtiles;
       row_begin = 0;
       row_end = p.M;
       m0 = mt * BM;
       n0 = nt * BN;
+      k_begin = split * p.k_chunk;
     }
     Bg = p.B + static_cast<int64_t>(g) * p.stride_bg;
   } else {
@@ -183,14 +203,19 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
     int local = L - g * per_group;
     int nt = local / p.m_tiles_max;
     int mt = local - nt * p.m_tiles_max;
-    row_end = p.offs ? min(max(p.offs[g], 0), p.rows) : p.rows;
-    row_begin = p.offs ? (g ? min(max(p.offs[g - 1], 0), row_end) : 0) : 0;
+    if (p.offs) {
+      row_end = min(max(p.offs[g], 0), p.rows);
+      row_begin = g ? min(max(p.offs[g - 1], 0), row_end) : 0;
+    } else {
+      row_begin = min(g * p.chunk_rows, p.rows);
+      row_end = min(row_begin + p.chunk_rows, p.rows);
+    }
     m0 = mt * BM;
     n0 = nt * BN;
   }
 
   // Reduction length for this tile.
-  const int Kred = (MODE == MODE_MG) ? p.K : (row_end - row_begin);
+  const int Kred = (MODE == MODE_MG) ? min(p.K - k_begin, p.k_chunk) : (row_end - row_begin);
 
   f32x16_t acc[SM][SN];
 #pragma unroll
@@ -213,11 +238,14 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (BM * BK / 32) / kThreads;
   constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (BN * BK / 32) / kThreads;
 
-  // Per-thread row pointers for K-contiguous operands (fixed over k).
-  const bf16_t* a_row_ptr[A_KCONTIG ? NLA : 1];
-  bool a_row_ok[A_KCONTIG ? NLA : 1];
-  const bf16_t* b_row_ptr[BK_CONTIG ? NLB : 1];
-  bool b_row_ok[BK_CONTIG ? NLB : 1];
+  // Buffer resources: A over all activation rows, B over this group's matrix.
+  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bg, p.b_bytes);
+
+  // Per-thread byte offsets of K-contiguous rows (fixed over k); kOOB marks
+  // rows outside the tile's valid range.
+  uint32_t a_row_off[A_KCONTIG ? NLA : 1];
+  uint32_t b_row_off[BK_CONTIG ? NLB : 1];
 
   if constexpr (A_KCONTIG) {
 #pragma unroll
@@ -225,8 +253,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       int c = tid + i * kThreads;
       int r = c / CH;
       int grow = m0 + r;
-      a_row_ok[i] = grow < row_end;
-      a_row_ptr[i] = p.A + static_cast<int64_t>(a_row_ok[i] ? grow : row_begin) * p.lda;
+      a_row_off[i] = grow < row_end ? static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u : kOOB;
     }
   }
   if constexpr (BK_CONTIG) {
@@ -250,8 +277,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         wrow = n0 + r;
         ok = wrow < p.N;
       }
-      b_row_ok[i] = ok;
-      b_row_ptr[i] = Bg + static_cast<int64_t>(ok ? wrow : 0) * p.ldb;
+      b_row_off[i] = ok ? static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u : kOOB;
     }
   }
 
@@ -265,7 +291,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       for (int i = 0; i < NLA; ++i) {
         int c = tid + i * kThreads;
         int kc = (c % CH) * 8;
-        ra[i] = ldg16(a_row_ptr[i] + k0 + kc, a_row_ok[i] && (k0 + kc) < Kred);
+        uint32_t off = (k0 + kc) < Kred ? a_row_off[i] + static_cast<uint32_t>(k_begin + k0 + kc) * 2u : kOOB;
+        ra[i] = bload16(rsA, off);
       }
     } else {
       // A is M-contiguous: tile = BK reduction rows x BM columns, 4x8 blocks.
@@ -280,7 +307,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         for (int q = 0; q < 4; ++q) {
           int kk = k0 + kb * 4 + q;
           bool ok = col_ok && kk < Kred;
-          ra[i * 4 + q] = ldg16(p.A + static_cast<int64_t>(row_begin + (ok ? kk : 0)) * p.lda + (ok ? col : 0), ok);
+          uint32_t off = ok ? (static_cast<uint32_t>(row_begin + kk) * static_cast<uint32_t>(p.lda) +
+                               static_cast<uint32_t>(col)) * 2u
+                            : kOOB;
+          ra[i * 4 + q] = bload16(rsA, off);
         }
       }
     }
@@ -290,7 +320,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       for (int i = 0; i < NLB; ++i) {
         int c = tid + i * kThreads;
         int kc = (c % CH) * 8;
-        rb[i] = ldg16(b_row_ptr[i] + k0 + kc, b_row_ok[i] && (k0 + kc) < Kred);
+        uint32_t off = (k0 + kc) < Kred ? b_row_off[i] + static_cast<uint32_t>(k_begin + k0 + kc) * 2u : kOOB;
+        rb[i] = bload16(rsB, off);
       }
     } else {
       constexpr int NBN = BN / 8;
@@ -304,8 +335,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         for (int q = 0; q < 4; ++q) {
           int kk = k0 + kb * 4 + q;
           bool ok = col_ok && kk < Kred;
-          int64_t rowi = (MODE == MODE_KG) ? static_cast<int64_t>(row_begin + (ok ? kk : 0)) : (ok ? kk : 0);
-          rb[i * 4 + q] = ldg16(Bg + rowi * p.ldb + (ok ? col : 0), ok);
+          int rowi = (MODE == MODE_KG) ? row_begin + kk : k_begin + kk;
+          uint32_t off = ok ? (static_cast<uint32_t>(rowi) * static_cast<uint32_t>(p.ldb) +
+                               static_cast<uint32_t>(col)) * 2u
+                            : kOOB;
+          rb[i * 4 + q] = bload16(rsB, off);
         }
       }
     }
@@ -446,8 +480,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
             o.y = pack_bf16x2(v2, v3);
             *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = o;
           } else if constexpr (EPI == EPI_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) =
-                make_float4(v0, v1, v2, v3);
+            *reinterpret_cast<float4*>(static_cast<float*>(p.C) + split * p.split_stride +
+                                       static_cast<int64_t>(row) * p.ldc + col) = make_float4(v0, v1, v2, v3);
           } else if constexpr (EPI == EPI_SWIGLU_BWD) {
             // v = d_act at (row, col..col+3); pre holds (gate | up).
             const bf16_t* pre = p.P + static_cast<int64_t>(row) * p.ldp;
@@ -507,12 +541,27 @@ constexpr int kBM = 128, kBN = 128, kBK = 64;
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
+constexpr int64_t kMaxRsrcBytes = (1ll << 31) - 64;
+
+int set_bytes(GemmParams& p, int64_t a_bytes, int64_t b_bytes, const char* name) {
+  MOE_REQUIRE(a_bytes < kMaxRsrcBytes && b_bytes < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED,
+              "%s: operand of %lld / %lld bytes exceeds the 2 GiB buffer-resource range", name, (long long)a_bytes,
+              (long long)b_bytes);
+  p.a_bytes = static_cast<uint32_t>(a_bytes);
+  p.b_bytes = static_cast<uint32_t>(b_bytes);
+  return MOE_OK;
+}
+
 template <int MODE, bool B_KCONTIG, int EPI>
 int launch(GemmParams& p, hipStream_t stream, const char* name) {
   int blocks;
+  if (p.k_splits < 1) {
+    p.k_splits = 1;
+    p.k_chunk = p.K;
+  }
   if (MODE == MODE_MG) {
     p.m_tiles_max = (p.M + kBM - 1) / kBM + (p.offs ? p.G : 0);
-    blocks = p.m_tiles_max * p.n_tiles;
+    blocks = p.m_tiles_max * p.n_tiles * (p.offs ? 1 : p.k_splits);
   } else {
     p.m_tiles_max = (p.M + kBM - 1) / kBM;
     blocks = p.G * p.m_tiles_max * p.n_tiles;
@@ -539,6 +588,55 @@ int check_common(const void* a, const void* b, const int32_t* offs, int64_t G, i
 }
 
 }  // namespace
+
+// Router logits as split-K partials: partials[s][T][E] (f32), s < splits, each
+// over the reduction range [s*k_chunk, (s+1)*k_chunk) of H.
+int router_logits_partials(const bf16_t* x, const bf16_t* wr, float* partials, int T, int H, int E, int splits,
+                           int k_chunk, hipStream_t stream) {
+  GemmParams p{};
+  p.A = x;
+  p.B = wr;
+  p.C = partials;
+  p.G = 1;
+  p.rows = p.M = T;
+  p.N = E;
+  p.K = H;
+  p.lda = H;
+  p.ldb = H;
+  p.ldc = E;
+  p.k_splits = splits;
+  p.k_chunk = k_chunk;
+  p.split_stride = static_cast<int64_t>(T) * E;
+  p.n_tiles = (E + kBN - 1) / kBN;
+  int rc = set_bytes(p, static_cast<int64_t>(T) * H * 2, static_cast<int64_t>(E) * H * 2, "router logits");
+  if (rc) return rc;
+  return launch<MODE_MG, true, EPI_F32>(p, stream, "router logits (split-K)");
+}
+
+// Router weight gradient as row-chunk partials: partials[c][E][H] (f32) over
+// rows [c*chunk_rows, (c+1)*chunk_rows) of T.
+int router_wgrad_partials(const bf16_t* dl, const bf16_t* x, float* partials, int T, int H, int E, int chunks,
+                          int chunk_rows, hipStream_t stream) {
+  GemmParams p{};
+  p.A = dl;
+  p.B = x;
+  p.C = partials;
+  p.offs = nullptr;
+  p.G = chunks;
+  p.chunk_rows = chunk_rows;
+  p.rows = T;
+  p.M = E;
+  p.N = H;
+  p.lda = E;
+  p.ldb = H;
+  p.ldc = H;
+  p.ldp = 1;  // f32 destination
+  p.stride_cg = static_cast<int64_t>(E) * H;
+  p.n_tiles = (H + kBN - 1) / kBN;
+  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(T) * H * 2, "router wgrad");
+  if (rc) return rc;
+  return launch<MODE_KG, false, EPI_WGRAD>(p, stream, "router wgrad (row chunks)");
+}
 
 }  // namespace moe
 
@@ -569,6 +667,7 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
   p.n_tiles = static_cast<int>((2 * I + kBN - 1) / kBN);
   // Each tile covers BN/2 act columns; the gate/up pairing needs I in whole sub-tiles.
   p.n_tiles = static_cast<int>((I + kBN / 2 - 1) / (kBN / 2));
+  if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
   return launch<MODE_MG, true, EPI_SWIGLU_FWD>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
 }
 
@@ -592,6 +691,7 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
   p.ldc = N;
   p.stride_bg = N * K;
   p.n_tiles = static_cast<int>((N + kBN - 1) / kBN);
+  if ((rc = set_bytes(p, M * K * 2, N * K * 2, "moe_grouped_gemm_fwd"))) return rc;
   return launch<MODE_MG, true, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_fwd");
 }
 
@@ -615,6 +715,7 @@ extern "C" int moe_router_logits_fwd(const void* x, const void* wr, float* logit
   p.ldb = H;
   p.ldc = E;
   p.n_tiles = static_cast<int>((E + kBN - 1) / kBN);
+  if ((rc = set_bytes(p, T * H * 2, E * H * 2, "moe_router_logits_fwd"))) return rc;
   return launch<MODE_MG, true, EPI_F32>(p, as_stream(stream), "moe_router_logits_fwd");
 }
 
@@ -639,6 +740,7 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   p.ldc = K;
   p.stride_bg = N * K;
   p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
+  if ((rc = set_bytes(p, M * N * 2, N * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
   return launch<MODE_MG, false, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
 }
 
@@ -667,6 +769,7 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   p.ldp = 2 * I;
   p.stride_bg = H * I;
   p.n_tiles = static_cast<int>((I + kBN - 1) / kBN);
+  if ((rc = set_bytes(p, M * H * 2, H * I * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
   return launch<MODE_MG, false, EPI_SWIGLU_BWD>(p, as_stream(stream), "moe_grouped_gemm_dgrad_swiglu_bwd");
 }
 
@@ -693,5 +796,6 @@ extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32
   p.stride_cg = N * K;
   p.accumulate = accumulate ? 1 : 0;
   p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
+  if ((rc = set_bytes(p, M * N * 2, M * K * 2, "moe_grouped_gemm_wgrad"))) return rc;
   return launch<MODE_KG, false, EPI_WGRAD>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
 }

@@ -8,7 +8,7 @@
 // Reference arithmetic: TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267
 // (router) and :514-593 (load_balancing_loss_func); the one-rank SP variant is
 // parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280.
-#include "common.h"
+#include "gemm.h"
 
 namespace moe {
 
@@ -106,6 +106,68 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_fwd_kernel(c
       scores[static_cast<int64_t>(t) * k + r] = norm ? pv[r] / tot : pv[r];
       indices[static_cast<int64_t>(t) * k + r] = sel[r];
     }
+  }
+}
+
+// logits[t] = sum_s partials[s][t] (+ bias), then the top-k softmax of that row.
+__global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kernel(
+    const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
+    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k, int norm) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int npl = (E + kWave - 1) / kWave;
+  const int64_t plane = static_cast<int64_t>(T) * E;
+  float v[kMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kMaxPerLane; ++j) {
+    int e = lane + j * kWave;
+    v[j] = -INFINITY;
+    if (j < npl && e < E) {
+      const float* src = partials + static_cast<int64_t>(t) * E + e;
+      float acc = 0.0f;
+      for (int sp = 0; sp < splits; ++sp) acc += src[sp * plane];
+      if (bias) acc += bias[e];
+      v[j] = acc;
+      logits[static_cast<int64_t>(t) * E + e] = acc;
+    }
+  }
+  SoftmaxStats st = softmax_stats(v, npl);
+  int sel[kMaxTopK];
+  float sl[kMaxTopK];
+  select_topk(v, npl, E, k, sel, sl);
+  float pv[kMaxTopK];
+  float tot = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < k) {
+      pv[r] = expf(sl[r] - st.max) / st.sum;
+      tot += pv[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < k && lane == r) {
+      scores[static_cast<int64_t>(t) * k + r] = norm ? pv[r] / tot : pv[r];
+      indices[static_cast<int64_t>(t) * k + r] = sel[r];
+    }
+  }
+}
+
+// out[i] = bf16(sum_c partials[c][i]) over n elements, fixed order.
+__global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, int chunks, int64_t n,
+                                            bf16_t* __restrict__ out) {
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x * 4) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c = 0; c < chunks; ++c) {
+      float4 v = *reinterpret_cast<const float4*>(partials + c * n + i);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    uint2 o;
+    o.x = pack_bf16x2(acc.x, acc.y);
+    o.y = pack_bf16x2(acc.z, acc.w);
+    *reinterpret_cast<uint2*>(out + i) = o;
   }
 }
 
@@ -240,35 +302,38 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_partial_kernel(const
   }
 }
 
-// Reduces the partials in block order; writes stats = (c_0..c_{E-1}, W), aux.
-__global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restrict__ ws, int nblk, int E,
+// Column sums of the per-block partials, fixed order: 64 entries per block,
+// wave w adds blocks w, w+4, ...; the 4 wave sums are combined in wave order.
+__global__ __launch_bounds__(256) void aux_reduce_kernel(const float* __restrict__ ws, int nblk, int n,
+                                                         float* __restrict__ sums) {
+  __shared__ float part[4][64];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int entry = blockIdx.x * 64 + lane;
+  float acc = 0.0f;
+  if (entry < n) {
+#pragma unroll 4
+    for (int b = wave; b < nblk; b += 4) acc += ws[static_cast<int64_t>(b) * n + entry];
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && entry < n) sums[entry] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+}
+
+// sums = (P_0..P_{E-1}, c_0..c_{E-1}, W) -> stats = (c, W), aux = E * sum_e (c_e/W)(P_e/W).
+__global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restrict__ sums, int E,
                                                              float* __restrict__ stats, float* __restrict__ aux) {
   __shared__ float terms[1024];
-  __shared__ float Wsh;
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    float W = 0.0f;
-    for (int b = 0; b < nblk; ++b) W += ws[static_cast<int64_t>(b) * (2 * E + 1) + 2 * E];
-    Wsh = W;
-    stats[E] = W;
+  const float W = sums[2 * E];
+  float term = 0.0f;
+  if (tid < E) {
+    float P = sums[tid], C = sums[E + tid];
+    stats[tid] = C;
+    term = (C / W) * (P / W);
   }
+  if (tid == 0) stats[E] = W;
+  terms[tid] = term;
   __syncthreads();
-  const float W = Wsh;
-  for (int e = tid; e < 1024; e += blockDim.x) {
-    float term = 0.0f;
-    if (e < E) {
-      float P = 0.0f, C = 0.0f;
-      for (int b = 0; b < nblk; ++b) {
-        P += ws[static_cast<int64_t>(b) * (2 * E + 1) + e];
-        C += ws[static_cast<int64_t>(b) * (2 * E + 1) + E + e];
-      }
-      stats[e] = C;
-      term = (C / W) * (P / W);
-    }
-    terms[e] = term;
-  }
-  __syncthreads();
-  // Fixed-shape tree over 1024 terms.
   for (int s = 512; s >= 1; s >>= 1) {
     if (tid < s) terms[tid] += terms[tid + s];
     __syncthreads();
@@ -361,7 +426,7 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
 
 extern "C" size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E) {
   if (T < 0 || E < 1) return 0;
-  return static_cast<size_t>(aux_blocks(T)) * static_cast<size_t>(2 * E + 1) * sizeof(float);
+  return static_cast<size_t>(aux_blocks(T) + 1) * static_cast<size_t>(2 * E + 1) * sizeof(float);
 }
 
 extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, int64_t T, int64_t E, int64_t k,
@@ -378,8 +443,13 @@ extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, 
                      token_weight, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), ws);
   rc = launch_status("moe_aux_loss_fwd(partial)");
   if (rc) return rc;
-  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, as_stream(stream), ws, nblk, static_cast<int>(E),
-                     stats, aux);
+  const int n = static_cast<int>(2 * E + 1);
+  float* sums = ws + static_cast<int64_t>(nblk) * n;
+  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64), dim3(256), 0, as_stream(stream), ws, nblk, n, sums);
+  rc = launch_status("moe_aux_loss_fwd(reduce)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, as_stream(stream), sums, static_cast<int>(E), stats,
+                     aux);
   return launch_status("moe_aux_loss_fwd(finalize)");
 }
 
@@ -394,4 +464,90 @@ extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, 
                      token_weight, stats, d_aux, static_cast<int>(T), static_cast<int>(E), d_logits,
                      accumulate ? 1 : 0);
   return launch_status("moe_aux_loss_bwd");
+}
+
+namespace {
+constexpr int kRouterWgradChunk = 256;  // rows per weight-gradient partial
+
+void router_split(int64_t T, int64_t H, int64_t E, int& splits, int& k_chunk) {
+  // Enough (M-tile, N-tile, K-split) work items to cover the CUs twice.
+  int64_t tiles = ((T + 127) / 128) * ((E + 127) / 128);
+  int64_t want = (512 + tiles - 1) / tiles;
+  int64_t max_splits = (H + 63) / 64;
+  if (want > max_splits) want = max_splits;
+  if (want < 1) want = 1;
+  k_chunk = static_cast<int>(((H + want - 1) / want + 63) / 64 * 64);
+  splits = static_cast<int>((H + k_chunk - 1) / k_chunk);
+}
+}  // namespace
+
+extern "C" size_t moe_router_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
+  if (T < 0 || H < 1 || E < 1) return 0;
+  int splits, k_chunk;
+  router_split(T, H, E, splits, k_chunk);
+  return static_cast<size_t>(splits) * static_cast<size_t>(T) * static_cast<size_t>(E) * sizeof(float);
+}
+
+extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_bias, float* logits, float* scores,
+                              int64_t* indices, int64_t T, int64_t H, int64_t E, int64_t k, int norm_topk_prob,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_router(T, E, k);
+  if (rc) return rc;
+  MOE_REQUIRE(x && wr && logits && scores && indices, MOE_ERR_INVALID, "router fwd: null pointer");
+  MOE_REQUIRE(H > 0 && H % 8 == 0 && E % 8 == 0 && aligned16(x) && aligned16(wr), MOE_ERR_UNSUPPORTED,
+              "router fwd: H (%lld) and E (%lld) must be multiples of 8 with 16-byte aligned operands",
+              (long long)H, (long long)E);
+  if (T == 0) return MOE_OK;
+  const size_t need = moe_router_fwd_workspace_bytes(T, H, E);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "router fwd: workspace %zu < %zu bytes",
+              workspace_bytes, need);
+  int splits, k_chunk;
+  router_split(T, H, E, splits, k_chunk);
+  float* partials = static_cast<float*>(workspace);
+  hipStream_t st = as_stream(stream);
+  rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
+                              static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
+  if (rc) return rc;
+  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
+  hipLaunchKernelGGL(router_reduce_topk_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits,
+                     logit_bias, logits, scores, indices, static_cast<int>(T), static_cast<int>(E),
+                     static_cast<int>(k), norm_topk_prob ? 1 : 0);
+  return launch_status("moe_router_fwd(reduce+topk)");
+}
+
+extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
+  if (T < 0 || H < 1 || E < 1) return 0;
+  int64_t chunks = (T + kRouterWgradChunk - 1) / kRouterWgradChunk;
+  if (chunks < 1) chunks = 1;
+  return static_cast<size_t>(chunks) * static_cast<size_t>(E) * static_cast<size_t>(H) * sizeof(float);
+}
+
+extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, const void* wr, void* dx, void* dwr,
+                                     int64_t T, int64_t H, int64_t E, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  MOE_REQUIRE(d_logits_bf16 && x && wr && dx && dwr, MOE_ERR_INVALID, "router logits bwd: null pointer");
+  MOE_REQUIRE(T >= 0 && H > 0 && E > 0 && H % 8 == 0 && E % 8 == 0, MOE_ERR_UNSUPPORTED,
+              "router logits bwd: H (%lld) and E (%lld) must be multiples of 8", (long long)H, (long long)E);
+  MOE_REQUIRE(aligned16(dwr), MOE_ERR_INVALID, "router logits bwd: dwr must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const size_t need = moe_router_logits_bwd_workspace_bytes(T, H, E);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
+              "router logits bwd: workspace %zu < %zu bytes", workspace_bytes, need);
+  const int chunks = static_cast<int>((T + kRouterWgradChunk - 1) / kRouterWgradChunk);
+  float* partials = static_cast<float*>(workspace);
+  int rc;
+  if (T > 0) {  // with no tokens the reduction below writes a zero gradient
+    rc = moe_grouped_gemm_dgrad(d_logits_bf16, wr, nullptr, 1, T, E, H, dx, stream);
+    if (rc) return rc;
+    rc = router_wgrad_partials(static_cast<const bf16_t*>(d_logits_bf16), static_cast<const bf16_t*>(x), partials,
+                               static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), chunks,
+                               kRouterWgradChunk, st);
+    if (rc) return rc;
+  }
+  const int64_t n = E * H;
+  int blocks = static_cast<int>((n / 4 + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(reduce_partials_bf16_kernel, dim3(blocks), dim3(256), 0, st, partials, chunks, n,
+                     static_cast<bf16_t*>(dwr));
+  return launch_status("moe_router_logits_bwd(reduce)");
 }

@@ -93,14 +93,12 @@ def router_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool,
     T, H = x.shape
     E = weight.shape[0]
     logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
-    s = _stream(x)
-    call("moe_router_logits_fwd", ptr(x), ptr(weight), ptr(logits), T, H, E, s, tag="router_logits")
-    if logit_bias is not None:
-        logits.add_(logit_bias.to(device=x.device, dtype=torch.float32))
     scores = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
     idx = torch.empty(T, top_k, dtype=torch.int64, device=x.device)
-    call("moe_router_topk_fwd", ptr(logits), ptr(scores), ptr(idx), T, E, top_k, int(norm_topk_prob), s,
-         tag="router_topk")
+    bias = None if logit_bias is None else logit_bias.to(device=x.device, dtype=torch.float32).contiguous()
+    ws = _ws(_lib.load().moe_router_fwd_workspace_bytes(T, H, E), x.device)
+    call("moe_router_fwd", ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(scores), ptr(idx), T, H, E, top_k,
+         int(norm_topk_prob), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
     return logits, scores, idx
 
 
@@ -132,9 +130,10 @@ def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_log
     call("moe_router_topk_bwd", ptr(logits), ptr(indices), ptr(d_scores), T, E, k, int(norm_topk_prob), ptr(dl),
          int(d_logits is not None), ptr(dl_bf16), s, tag="router_topk_bwd")
     dx = torch.empty(T, H, dtype=BF16, device=x.device)
-    call("moe_grouped_gemm_dgrad", ptr(dl_bf16), ptr(weight), None, 1, T, E, H, ptr(dx), s, tag="router_dgrad")
     dw = torch.empty(E, H, dtype=weight.dtype, device=x.device)
-    call("moe_grouped_gemm_wgrad", ptr(dl_bf16), ptr(x), None, 1, T, E, H, ptr(dw), 0, 0, s, tag="router_wgrad")
+    ws = _ws(_lib.load().moe_router_logits_bwd_workspace_bytes(T, H, E), x.device)
+    call("moe_router_logits_bwd", ptr(dl_bf16), ptr(x), ptr(weight), ptr(dx), ptr(dw), T, H, E, ptr(ws), ws.numel(),
+         s, tag="router_gemm_bwd")
     return dx, dw
 
 

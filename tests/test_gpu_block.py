@@ -164,7 +164,6 @@ def test_transformers_block_runs_on_the_plugin():
             p.normal_(0, 0.05)
     ref_block = Qwen3MoeSparseMoeBlock(cfg)
     ref_block.load_state_dict(block.state_dict())
-    ref_block.config._experts_implementation = "eager"
     block = block.to(DEV, BF)
     x = torch.randn(2, 64, 256)
     xg = x.to(DEV, BF).requires_grad_()

@@ -214,7 +214,7 @@ def test_grouped_gemm_fwd(name, cnt, N, K):
     a = torch.randn(M, K, generator=gen(1)).to(BF)
     w = (torch.randn(G, N, K, generator=gen(2)) * 0.05).to(BF)
     c = torch.full((M, N), 7.0, dtype=BF, device=DEV)
-    _lib.call("moe_grouped_gemm_fwd", a.to(DEV).data_ptr(), (wd := w.to(DEV)).data_ptr(),
+    _lib.call("moe_grouped_gemm_fwd", (ad := a.to(DEV)).data_ptr(), (wd := w.to(DEV)).data_ptr(),
               (od := offs.to(DEV)).data_ptr(), G, M, N, K, c.data_ptr(), _lib.stream_of(c))
     torch.cuda.synchronize()
     n = int(counts.sum())
