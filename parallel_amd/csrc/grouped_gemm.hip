@@ -65,23 +65,30 @@ __device__ __forceinline__ uint32_t sel_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-// Column c (0..7) of a 4x8 bf16 block given as four 16-byte rows, returned as
-// 4 bf16 (k = 0..3) in two dwords.
-__device__ __forceinline__ uint2 column4(const uint4 (&v)[4], int c) {
-  uint32_t w0, w1, w2, w3;
-  switch (c >> 1) {
-    case 0: w0 = v[0].x; w1 = v[1].x; w2 = v[2].x; w3 = v[3].x; break;
-    case 1: w0 = v[0].y; w1 = v[1].y; w2 = v[2].y; w3 = v[3].y; break;
-    case 2: w0 = v[0].z; w1 = v[1].z; w2 = v[2].z; w3 = v[3].z; break;
-    default: w0 = v[0].w; w1 = v[1].w; w2 = v[2].w; w3 = v[3].w; break;
+// Column c (0..7) of an 8x8 bf16 block given as eight 16-byte rows (row = k),
+// returned as 8 bf16 (k = 0..7) in one 16-byte vector.
+__device__ __forceinline__ uint4 column8(const uint4* v, int c) {
+  uint32_t w[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    switch (c >> 1) {
+      case 0: w[q] = v[q].x; break;
+      case 1: w[q] = v[q].y; break;
+      case 2: w[q] = v[q].z; break;
+      default: w[q] = v[q].w; break;
+    }
   }
-  uint2 r;
+  uint4 r;
   if (c & 1) {
-    r.x = sel_hi(w0, w1);
-    r.y = sel_hi(w2, w3);
+    r.x = sel_hi(w[0], w[1]);
+    r.y = sel_hi(w[2], w[3]);
+    r.z = sel_hi(w[4], w[5]);
+    r.w = sel_hi(w[6], w[7]);
   } else {
-    r.x = sel_lo(w0, w1);
-    r.y = sel_lo(w2, w3);
+    r.x = sel_lo(w[0], w[1]);
+    r.y = sel_lo(w[2], w[3]);
+    r.z = sel_lo(w[4], w[5]);
+    r.w = sel_lo(w[6], w[7]);
   }
   return r;
 }
@@ -234,9 +241,21 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
 
   // ------------------------------------------------------ loaders
   // K-contiguous operand: R rows x BK, 16-byte chunks.
+  // K-contiguous operand: 16-byte chunks, chunk c -> (row c / CH, k-chunk c % CH).
+  // M/N-contiguous operand: 8x8 blocks, block b -> (k-chunk b % CH, mn-block b / CH);
+  // the k-chunk varies fastest across lanes, which makes each global load a
+  // 128-byte run per row and the transposed 16-byte LDS stores conflict-free.
+  // When both operands are transposed (weight gradient) A uses waves 0-1 and B
+  // waves 2-3.
   constexpr int CH = BK / 8;
-  constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (BM * BK / 32) / kThreads;
-  constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (BN * BK / 32) / kThreads;
+  constexpr int NBA = A_KCONTIG ? 0 : CH * (BM / 8);  // 8x8 blocks of A
+  constexpr int NBB = BK_CONTIG ? 0 : CH * (BN / 8);
+  constexpr int A_TOFF = 0;
+  constexpr int B_TOFF = (!A_KCONTIG && !BK_CONTIG) ? kThreads / 2 : 0;
+  constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (NBA + kThreads - 1) / kThreads;
+  constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (NBB + kThreads - 1) / kThreads;
+  static_assert(A_KCONTIG || NBA % kWave == 0, "A block count must be whole waves");
+  static_assert(BK_CONTIG || NBB % kWave == 0, "B block count must be whole waves");
 
   // Buffer resources: A over all activation rows, B over this group's matrix.
   const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
@@ -281,8 +300,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
     }
   }
 
-  uint4 ra[A_KCONTIG ? NLA : NLA * 4];
-  uint4 rb[BK_CONTIG ? NLB : NLB * 4];
+  uint4 ra[A_KCONTIG ? NLA : NLA * 8];
+  uint4 rb[BK_CONTIG ? NLB : NLB * 8];
 
   auto load_tile = [&](int k0) {
     // A
@@ -295,22 +314,23 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         ra[i] = bload16(rsA, off);
       }
     } else {
-      // A is M-contiguous: tile = BK reduction rows x BM columns, 4x8 blocks.
-      constexpr int NBM = BM / 8;
+      // A is M-contiguous: tile = BK reduction rows x BM columns, 8x8 blocks.
 #pragma unroll
       for (int i = 0; i < NLA; ++i) {
-        int blk = tid + i * kThreads;
-        int mb = blk % NBM, kb = blk / NBM;
-        int col = m0 + mb * 8;
-        bool col_ok = col < p.M;
+        int blk = ((tid + A_TOFF) % kThreads) + i * kThreads;
+        if (blk < NBA) {
+          int kc = blk % CH, mb = blk / CH;
+          int col = m0 + mb * 8;
+          bool col_ok = col < p.M;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          int kk = k0 + kb * 4 + q;
-          bool ok = col_ok && kk < Kred;
-          uint32_t off = ok ? (static_cast<uint32_t>(row_begin + kk) * static_cast<uint32_t>(p.lda) +
-                               static_cast<uint32_t>(col)) * 2u
-                            : kOOB;
-          ra[i * 4 + q] = bload16(rsA, off);
+          for (int q = 0; q < 8; ++q) {
+            int kk = k0 + kc * 8 + q;
+            bool ok = col_ok && kk < Kred;
+            uint32_t off = ok ? (static_cast<uint32_t>(row_begin + kk) * static_cast<uint32_t>(p.lda) +
+                                 static_cast<uint32_t>(col)) * 2u
+                              : kOOB;
+            ra[i * 8 + q] = bload16(rsA, off);
+          }
         }
       }
     }
@@ -324,22 +344,23 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         rb[i] = bload16(rsB, off);
       }
     } else {
-      constexpr int NBN = BN / 8;
 #pragma unroll
       for (int i = 0; i < NLB; ++i) {
-        int blk = tid + i * kThreads;
-        int nbk = blk % NBN, kb = blk / NBN;
-        int col = n0 + nbk * 8;
-        bool col_ok = col < p.N;
+        int blk = ((tid + B_TOFF) % kThreads) + i * kThreads;
+        if (blk < NBB) {
+          int kc = blk % CH, nb8 = blk / CH;
+          int col = n0 + nb8 * 8;
+          bool col_ok = col < p.N;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          int kk = k0 + kb * 4 + q;
-          bool ok = col_ok && kk < Kred;
-          int rowi = (MODE == MODE_KG) ? row_begin + kk : k_begin + kk;
-          uint32_t off = ok ? (static_cast<uint32_t>(rowi) * static_cast<uint32_t>(p.ldb) +
-                               static_cast<uint32_t>(col)) * 2u
-                            : kOOB;
-          rb[i * 4 + q] = bload16(rsB, off);
+          for (int q = 0; q < 8; ++q) {
+            int kk = k0 + kc * 8 + q;
+            bool ok = col_ok && kk < Kred;
+            int rowi = (MODE == MODE_KG) ? row_begin + kk : k_begin + kk;
+            uint32_t off = ok ? (static_cast<uint32_t>(rowi) * static_cast<uint32_t>(p.ldb) +
+                                 static_cast<uint32_t>(col)) * 2u
+                              : kOOB;
+            rb[i * 8 + q] = bload16(rsB, off);
+          }
         }
       }
     }
@@ -356,15 +377,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         *reinterpret_cast<uint4*>(as + r * LDS_STRIDE + kc) = ra[i];
       }
     } else {
-      constexpr int NBM = BM / 8;
 #pragma unroll
       for (int i = 0; i < NLA; ++i) {
-        int blk = tid + i * kThreads;
-        int mb = blk % NBM, kb = blk / NBM;
-        uint4 v[4] = {ra[i * 4 + 0], ra[i * 4 + 1], ra[i * 4 + 2], ra[i * 4 + 3]};
+        int blk = ((tid + A_TOFF) % kThreads) + i * kThreads;
+        if (blk < NBA) {
+          int kc = blk % CH, mb = blk / CH;
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-          *reinterpret_cast<uint2*>(as + (mb * 8 + c) * LDS_STRIDE + kb * 4) = column4(v, c);
+          for (int c = 0; c < 8; ++c)
+            *reinterpret_cast<uint4*>(as + (mb * 8 + c) * LDS_STRIDE + kc * 8) = column8(ra + i * 8, c);
+        }
       }
     }
     if constexpr (BK_CONTIG) {
@@ -375,15 +396,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
         *reinterpret_cast<uint4*>(bs + r * LDS_STRIDE + kc) = rb[i];
       }
     } else {
-      constexpr int NBN = BN / 8;
 #pragma unroll
       for (int i = 0; i < NLB; ++i) {
-        int blk = tid + i * kThreads;
-        int nbk = blk % NBN, kb = blk / NBN;
-        uint4 v[4] = {rb[i * 4 + 0], rb[i * 4 + 1], rb[i * 4 + 2], rb[i * 4 + 3]};
+        int blk = ((tid + B_TOFF) % kThreads) + i * kThreads;
+        if (blk < NBB) {
+          int kc = blk % CH, nb8 = blk / CH;
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-          *reinterpret_cast<uint2*>(bs + (nbk * 8 + c) * LDS_STRIDE + kb * 4) = column4(v, c);
+          for (int c = 0; c < 8; ++c)
+            *reinterpret_cast<uint4*>(bs + (nb8 * 8 + c) * LDS_STRIDE + kc * 8) = column8(rb + i * 8, c);
+        }
       }
     }
   };
