@@ -104,7 +104,19 @@ def main() -> int:
     ap.add_argument("--config", default="c2", help="workload key (c2 c3 c4 c5); c2 is the headline")
     ap.add_argument("--cpu-baseline-tokens", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 1 GiB three times")
+        return 0
     if args.gpus != 1:
         print(
             f"bench.py runs one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "

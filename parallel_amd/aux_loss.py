@@ -32,7 +32,10 @@ def load_balancing_loss_func(
     if gate_logits is None or not isinstance(gate_logits, tuple):
         return 0
     device = gate_logits[0].device
-    logits = torch.cat([g.to(device) for g in gate_logits], dim=0)
+    if len(gate_logits) == 1:
+        logits = gate_logits[0]
+    else:
+        logits = torch.cat([g.to(device) for g in gate_logits], dim=0)
     if num_experts is None:
         num_experts = logits.shape[-1]
     token_weight = None
@@ -55,5 +58,5 @@ def sequence_parallel_load_balancing_loss(
     if not router_logits:
         return None
     require_single_rank(group, "sequence-parallel load-balancing loss")
-    logits = torch.cat(tuple(router_logits), dim=0)
+    logits = router_logits[0] if len(router_logits) == 1 else torch.cat(tuple(router_logits), dim=0)
     return _aux(logits, num_experts, top_k, None)

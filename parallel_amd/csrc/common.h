@@ -36,16 +36,68 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Wave-wide reductions over 64 lanes (butterfly via ds_swizzle-free shuffles).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+// Wave-wide reductions over 64 lanes with DPP lane movement (register-level,
+// no LDS round trip): quad xor-1, quad xor-2, half-row mirror, row mirror,
+// then row_bcast15 / row_bcast31 fold rows 0-1 and 2-3 into row 3; lane 63
+// holds the result, which readlane makes wave-uniform.
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;
+constexpr int kMirror = 0x140;
+constexpr int kBcast15 = 0x142;   // lane 15 of row r -> row r+1 (rows 1, 3 enabled)
+constexpr int kBcast31 = 0x143;   // lane 31 -> rows 2, 3
+}  // namespace dpp
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_move(float old, float src) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, ROW_MASK, 0xF, false));
 }
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_move_i(int old, int src) {
+  return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, 0xF, false);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_move<dpp::kQuadXor1>(0.0f, v);
+  v += dpp_move<dpp::kQuadXor2>(0.0f, v);
+  v += dpp_move<dpp::kHalfMirror>(0.0f, v);
+  v += dpp_move<dpp::kMirror>(0.0f, v);
+  v += dpp_move<dpp::kBcast15, 0xA>(0.0f, v);
+  v += dpp_move<dpp::kBcast31, 0xC>(0.0f, v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dpp_move<dpp::kQuadXor1>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kQuadXor2>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kHalfMirror>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kMirror>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kBcast15, 0xA>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kBcast31, 0xC>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Wave arg-max of (value, index): larger value wins, ties go to the lower
+// index.  Lanes outside a row mask keep their own pair (old == self).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  float ov = dpp_move<CTRL, ROW_MASK>(v, v);
+  int oi = dpp_move_i<CTRL, ROW_MASK>(i, i);
+  bool take = ov > v || (ov == v && oi < i);
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  argmax_step<dpp::kQuadXor1>(v, i);
+  argmax_step<dpp::kQuadXor2>(v, i);
+  argmax_step<dpp::kHalfMirror>(v, i);
+  argmax_step<dpp::kMirror>(v, i);
+  argmax_step<dpp::kBcast15, 0xA>(v, i);
+  argmax_step<dpp::kBcast31, 0xC>(v, i);
+  v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  i = __builtin_amdgcn_readlane(i, 63);
 }
 
 // Inclusive prefix sum across the wave (Hillis-Steele over 6 steps).

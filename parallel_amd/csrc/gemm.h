@@ -13,4 +13,7 @@ int router_logits_partials(const bf16_t* x, const bf16_t* wr, float* partials, i
 int router_wgrad_partials(const bf16_t* dl, const bf16_t* x, float* partials, int T, int H, int E, int chunks,
                           int chunk_rows, hipStream_t stream);
 
+// dx[T,H] (bf16) = dl[T,E] . wr[E,H].
+int router_dgrad(const bf16_t* dl, const bf16_t* wr, bf16_t* dx, int T, int H, int E, hipStream_t stream);
+
 }  // namespace moe

@@ -7,13 +7,19 @@
 // MG = groups partition the rows of the activation operand (variable M per
 // expert), KG = groups partition the reduction (variable K per expert).
 //
-// Tiling: 256 threads = 4 waves in a 2x2 grid; each wave owns a
-// (BM/2)x(BN/2) block of 32x32 MFMA sub-tiles (v_mfma_f32_32x32x16_bf16).
-// Operands are staged through LDS as K-contiguous rows (row stride BK+8 to
-// spread banks) with double buffering and register prefetch of the next
+// Tiling: WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of 32x32
+// MFMA sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators in AGPRs).
+// The expert GEMMs use 256x256x64 tiles on 8 waves (two waves per SIMD, one
+// workgroup per CU, 144 KiB of LDS); the small router GEMMs use 128x128x64 on
+// 4 waves.  Operands are staged through LDS as K-contiguous rows (row stride
+// BK+8 elements) with double buffering and register prefetch of the next
 // k-tile.  Operands that are contiguous along M/N in HBM are transposed in
-// registers (4x8 bf16 blocks, v_perm) on their way into LDS so every MFMA
-// fragment read is one 16-byte ds_read.
+// registers (8x8 bf16 blocks, v_perm) on their way into LDS so every MFMA
+// fragment read is one 16-byte ds_read.  Global reads are raw buffer loads:
+// offsets past the resource size read as zero, so ragged rows and the K tail
+// need no branches.  Sub-tiles of a wave that lie wholly outside the valid
+// rows/columns skip their fragment reads and MFMAs (the last M tile of an
+// expert is usually short).
 //
 // Tiles are mapped to groups on the device from the `offs` cumsum (no host
 // sync).  The logical tile order is group-major, then n-tile, then m-tile, so
@@ -21,7 +27,7 @@
 // the launch index is remapped so that each XCD (blocks are dealt round-robin
 // over the 8 XCDs) gets a contiguous run of logical tiles and the sharing
 // happens in that XCD's L2.
-#include <stdarg.h>
+#include <type_traits>
 
 #include "gemm.h"
 
@@ -30,7 +36,6 @@ namespace moe {
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU_FWD = 2, EPI_SWIGLU_BWD = 3, EPI_WGRAD = 4 };
 enum { MODE_MG = 0, MODE_KG = 1 };
 
-constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
 
 struct GemmParams {
@@ -41,18 +46,18 @@ struct GemmParams {
   const bf16_t* P;  // SWIGLU_BWD: saved pre-activation [rows, 2N]
   const int32_t* offs;
   int G;
-  int rows;  // total activation rows (M for MG; sum of K for KG)
+  int rows;     // total activation rows (M for MG; sum of K for KG)
   int M, N, K;  // GEMM-internal sizes: MG: M = rows, N out cols, K reduction; KG: M x N output per group
   int64_t lda, ldb, ldc, ldp;
   int64_t stride_bg, stride_cg;
   uint32_t a_bytes;  // bytes addressable through the A buffer resource
   uint32_t b_bytes;  // bytes of one group's B (MG) or of all of B (KG)
-  int swiglu_I;  // SWIGLU_FWD: intermediate size I (weight rows gate: [0,I), up: [I,2I))
+  int swiglu_I;      // SWIGLU_FWD: intermediate size I (weight rows gate: [0,I), up: [I,2I))
   int accumulate;
   int n_tiles, m_tiles_max, total_blocks;
-  int k_splits, k_chunk;   // MG without groups: split the reduction, partial outputs stacked
-  int64_t split_stride;    // elements between split partials of C
-  int chunk_rows;          // KG without offs and G > 1: group g = rows [g*chunk_rows, ...)
+  int k_splits, k_chunk;  // MG without groups: split the reduction, partial outputs stacked
+  int64_t split_stride;   // elements between split partials of C
+  int chunk_rows;         // KG without offs and G > 1: group g = rows [g*chunk_rows, ...)
 };
 
 // ---------------------------------------------------------------- helpers
@@ -131,30 +136,46 @@ __device__ __forceinline__ bool locate_group(const int32_t* offs, int G, int row
     int incl = wave_inclusive_scan(nt);
     unsigned long long hit = __ballot(g < G && L < base + incl);
     if (hit) {
-      int src = __ffsll(hit) - 1;
+      // Results are wave-uniform: move them to scalar registers so the
+      // compiler sees uniform control flow downstream.
+      int src = __ffsll(static_cast<long long>(hit)) - 1;
       int excl = incl - nt;
-      g_out = c0 + src;
-      tile0_out = base + __shfl(excl, src, kWave);
-      row0_out = __shfl(lo, src, kWave);
-      cnt_out = __shfl(cnt, src, kWave);
+      g_out = __builtin_amdgcn_readfirstlane(c0 + src);
+      tile0_out = __builtin_amdgcn_readfirstlane(base + __builtin_amdgcn_readlane(excl, src));
+      row0_out = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(lo, src));
+      cnt_out = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(cnt, src));
       return true;
     }
-    base += __shfl(incl, kWave - 1, kWave);
+    base += __builtin_amdgcn_readlane(incl, kWave - 1);
   }
   return false;
 }
 
+// Tile configurations.
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct TileCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int kThreads = 64 * WM * WN;
+};
+using BigTile = TileCfg<256, 256, 64, 2, 4>;    // expert GEMMs
+using SmallTile = TileCfg<128, 128, 64, 2, 2>;  // router GEMMs (N = E = 128)
+
 // ------------------------------------------------------------------ kernel
 
-template <int MODE, bool B_KCONTIG, int EPI, int BM, int BN, int BK>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams p) {
+template <int MODE, bool B_KCONTIG, int EPI, class CFG>
+__global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmParams p) {
+  constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN;
+  constexpr int kThreads = CFG::kThreads;
   constexpr int LDS_STRIDE = BK + 8;  // elements
-  constexpr int SM = BM / 64;         // 32x32 sub-tiles per wave along M
-  constexpr int SN = BN / 64;         // ... along N
-  constexpr int A_KCONTIG = (MODE == MODE_MG);
+  constexpr int WTM = BM / WM;        // wave tile rows
+  constexpr int WTN = BN / WN;        // wave tile cols
+  constexpr int SM = WTM / 32;        // 32x32 sub-tiles per wave along M
+  constexpr int SN = WTN / 32;        // ... along N
+  constexpr bool A_KCONTIG = (MODE == MODE_MG);
   constexpr bool BK_CONTIG = (MODE == MODE_MG) && B_KCONTIG;
   static_assert(BK % 16 == 0, "BK must be a multiple of the MFMA K (16)");
-  static_assert((BM * BK) % (8 * kThreads) == 0 && (BN * BK) % (8 * kThreads) == 0, "tile too small for loader");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 sub-tiles");
+  static_assert((BM * BK / 8) % kThreads == 0 && (BN * BK / 8) % kThreads == 0, "tile too small for loader");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
 
   __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDS_STRIDE];
@@ -163,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
 
   // XCD-aware remap of the launch index to a logical tile index.
   const int nb = p.total_blocks;  // multiple of kNumXcd
@@ -171,8 +192,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   const int L = (bid % kNumXcd) * (nb / kNumXcd) + bid / kNumXcd;
 
   // ------------------------------------------------------ tile -> work
-  int g, m0, n0;             // group, first output row (within group for KG), first output col
-  int row_begin, row_end;    // MG: absolute activation rows of the group; KG: reduction rows
+  int g, m0, n0;               // group, first output row (within group for KG), first output col
+  int row_begin, row_end;      // MG: absolute activation rows of the group; KG: reduction rows
   int split = 0, k_begin = 0;  // split-K partial index and its first reduction index
   const bf16_t* Bg = p.B;
   if constexpr (MODE == MODE_MG) {
@@ -224,6 +245,23 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   // Reduction length for this tile.
   const int Kred = (MODE == MODE_MG) ? min(p.K - k_begin, p.k_chunk) : (row_end - row_begin);
 
+  if constexpr (MODE == MODE_KG) {
+    // Empty group: the weight gradient is zero (written below) or, when
+    // accumulating, unchanged.
+    if (Kred <= 0 && p.accumulate) return;
+  }
+
+  // Valid rows / columns of this wave's tile -> active 32x32 sub-tiles
+  // (wave-uniform; inactive sub-tiles skip their fragment reads and MFMAs).
+  // A SwiGLU tile keeps every sub-tile: gate and up halves pair up by index.
+  const int row_limit = (MODE == MODE_MG) ? row_end : p.M;
+  const int wrow0 = m0 + wm * WTM;
+  const int wcol0 = n0 + wn * WTN;
+  const int act_sm = __builtin_amdgcn_readfirstlane(min(SM, max(0, (row_limit - wrow0 + 31) / 32)));
+  const int act_sn =
+      __builtin_amdgcn_readfirstlane((EPI == EPI_SWIGLU_FWD) ? SN : min(SN, max(0, (p.N - wcol0 + 31) / 32)));
+  const bool full_tile = (act_sm == SM) && (act_sn == SN);
+
   f32x16_t acc[SM][SN];
 #pragma unroll
   for (int i = 0; i < SM; ++i)
@@ -232,26 +270,18 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  if constexpr (MODE == MODE_KG) {
-    if (Kred <= 0) {
-      // Empty group: the weight gradient is zero.
-      if (p.accumulate) return;
-    }
-  }
-
   // ------------------------------------------------------ loaders
-  // K-contiguous operand: R rows x BK, 16-byte chunks.
   // K-contiguous operand: 16-byte chunks, chunk c -> (row c / CH, k-chunk c % CH).
   // M/N-contiguous operand: 8x8 blocks, block b -> (k-chunk b % CH, mn-block b / CH);
   // the k-chunk varies fastest across lanes, which makes each global load a
   // 128-byte run per row and the transposed 16-byte LDS stores conflict-free.
-  // When both operands are transposed (weight gradient) A uses waves 0-1 and B
-  // waves 2-3.
+  // A transposed operand is loaded by the first half of the threads and a
+  // transposed B by the second half.
   constexpr int CH = BK / 8;
   constexpr int NBA = A_KCONTIG ? 0 : CH * (BM / 8);  // 8x8 blocks of A
   constexpr int NBB = BK_CONTIG ? 0 : CH * (BN / 8);
   constexpr int A_TOFF = 0;
-  constexpr int B_TOFF = (!A_KCONTIG && !BK_CONTIG) ? kThreads / 2 : 0;
+  constexpr int B_TOFF = BK_CONTIG ? 0 : kThreads / 2;
   constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (NBA + kThreads - 1) / kThreads;
   constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (NBB + kThreads - 1) / kThreads;
   static_assert(A_KCONTIG || NBA % kWave == 0, "A block count must be whole waves");
@@ -283,13 +313,13 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       int wrow;
       bool ok;
       if constexpr (EPI == EPI_SWIGLU_FWD) {
-        // Tile row r -> (wave column, sub-tile, half): first SN/2 sub-tiles of
-        // each wave column are gate rows, the rest the matching up rows.
-        int wcol = r / (BN / 2);
-        int within = r % (BN / 2);
+        // Tile row r -> (wave column, sub-tile, half): the first SN/2 sub-tiles
+        // of each wave column are gate rows, the rest the matching up rows.
+        int wcol = r / WTN;
+        int within = r % WTN;
         int sn = within / 32;
         int half = sn / (SN / 2);
-        int act_col = (n0 / 2) + wcol * (BN / 4) + (sn % (SN / 2)) * 32 + (within % 32);
+        int act_col = (n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
         ok = act_col < p.swiglu_I;
         wrow = half * p.swiglu_I + act_col;
       } else {
@@ -412,57 +442,65 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
   const int frag_row = lane & 31;
   const int frag_k = (lane >> 5) * 8;
 
-  auto compute_tile = [&](int buf) {
-    const bf16_t* as = As[buf] + (wm * (BM / 2) + frag_row) * LDS_STRIDE + frag_k;
-    const bf16_t* bs = Bs[buf] + (wn * (BN / 2) + frag_row) * LDS_STRIDE + frag_k;
+  // FULL: every sub-tile active, no control flow between the fragment reads
+  // and the MFMAs; otherwise skip the inactive sub-tiles (uniform branches).
+  auto compute_tile = [&](int buf, auto full) {
+    constexpr bool FULL = decltype(full)::value;
+    const bf16_t* as = As[buf] + (wm * WTM + frag_row) * LDS_STRIDE + frag_k;
+    const bf16_t* bs = Bs[buf] + (wn * WTN + frag_row) * LDS_STRIDE + frag_k;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[SM], bfr[SN];
 #pragma unroll
-      for (int i = 0; i < SM; ++i) af[i] = *reinterpret_cast<const bf16x8_t*>(as + i * 32 * LDS_STRIDE + ks * 16);
+      for (int i = 0; i < SM; ++i)
+        if (FULL || i < act_sm) af[i] = *reinterpret_cast<const bf16x8_t*>(as + i * 32 * LDS_STRIDE + ks * 16);
 #pragma unroll
-      for (int j = 0; j < SN; ++j) bfr[j] = *reinterpret_cast<const bf16x8_t*>(bs + j * 32 * LDS_STRIDE + ks * 16);
+      for (int j = 0; j < SN; ++j)
+        if (FULL || j < act_sn) bfr[j] = *reinterpret_cast<const bf16x8_t*>(bs + j * 32 * LDS_STRIDE + ks * 16);
 #pragma unroll
       for (int i = 0; i < SM; ++i)
 #pragma unroll
         for (int j = 0; j < SN; ++j)
           // Operands swapped: the result holds C^T fragments, so each lane
           // owns one output row and runs of 4 consecutive output columns.
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+          if (FULL || (i < act_sm && j < act_sn))
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     }
   };
 
-  const int nk = (Kred + BK - 1) / BK;
-  if (nk > 0) {
+  auto main_loop = [&](auto full) {
+    const int nk = (Kred + BK - 1) / BK;
+    if (nk <= 0) return;
     load_tile(0);
     store_tile(0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
       if (kt + 1 < nk) load_tile((kt + 1) * BK);
-      compute_tile(cur);
+      compute_tile(cur, full);
       if (kt + 1 < nk) store_tile(cur ^ 1);
       __syncthreads();
     }
-  }
+  };
+  if (full_tile)
+    main_loop(std::true_type{});
+  else
+    main_loop(std::false_type{});
 
   // ------------------------------------------------------ epilogue
-  // Lane owns output row  wm*(BM/2) + i*32 + (lane & 31)  and columns
-  // wn*(BN/2) + j*32 + 8*q + 4*(lane >> 5) + {0..3} holding acc[i][j][4q..4q+3].
+  // Lane owns output row  wrow0 + i*32 + (lane & 31)  and columns
+  // wcol0 + j*32 + 8*q + 4*(lane >> 5) + {0..3} holding acc[i][j][4q..4q+3].
   const int col_lane = 4 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < SM; ++i) {
-    const int row = m0 + wm * (BM / 2) + i * 32 + (lane & 31);
-    bool row_ok;
-    if constexpr (MODE == MODE_MG) row_ok = row < row_end;
-    else row_ok = row < p.M;
-    if (!row_ok) continue;
+    const int row = wrow0 + i * 32 + (lane & 31);
+    if (row >= row_limit) continue;
     if constexpr (EPI == EPI_SWIGLU_FWD) {
 #pragma unroll
       for (int j = 0; j < SN / 2; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int col = (n0 / 2) + wn * (BN / 4) + j * 32 + 8 * q + col_lane;
+          const int col = (n0 / 2) + wn * (WTN / 2) + j * 32 + 8 * q + col_lane;
           if (col >= p.swiglu_I) continue;
           float gt[4], up[4];
 #pragma unroll
@@ -491,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
       for (int j = 0; j < SN; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int col = n0 + wn * (BN / 2) + j * 32 + 8 * q + col_lane;
+          const int col = wcol0 + j * 32 + 8 * q + col_lane;
           if (col >= p.N) continue;
           float v0 = acc[i][j][4 * q + 0], v1 = acc[i][j][4 * q + 1];
           float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
@@ -558,8 +596,6 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(const GemmParams
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 constexpr int64_t kMaxRsrcBytes = (1ll << 31) - 64;
@@ -573,24 +609,27 @@ int set_bytes(GemmParams& p, int64_t a_bytes, int64_t b_bytes, const char* name)
   return MOE_OK;
 }
 
-template <int MODE, bool B_KCONTIG, int EPI>
+template <int MODE, bool B_KCONTIG, int EPI, class CFG>
 int launch(GemmParams& p, hipStream_t stream, const char* name) {
-  int blocks;
   if (p.k_splits < 1) {
     p.k_splits = 1;
     p.k_chunk = p.K;
   }
+  // Output column tiles; a SwiGLU tile covers BN/2 act columns (gate + up rows).
+  p.n_tiles = (EPI == EPI_SWIGLU_FWD) ? (p.swiglu_I + CFG::BN / 2 - 1) / (CFG::BN / 2)
+                                      : (p.N + CFG::BN - 1) / CFG::BN;
+  int64_t blocks;
   if (MODE == MODE_MG) {
-    p.m_tiles_max = (p.M + kBM - 1) / kBM + (p.offs ? p.G : 0);
-    blocks = p.m_tiles_max * p.n_tiles * (p.offs ? 1 : p.k_splits);
+    p.m_tiles_max = (p.M + CFG::BM - 1) / CFG::BM + (p.offs ? p.G : 0);
+    blocks = static_cast<int64_t>(p.m_tiles_max) * p.n_tiles * (p.offs ? 1 : p.k_splits);
   } else {
-    p.m_tiles_max = (p.M + kBM - 1) / kBM;
-    blocks = p.G * p.m_tiles_max * p.n_tiles;
+    p.m_tiles_max = (p.M + CFG::BM - 1) / CFG::BM;
+    blocks = static_cast<int64_t>(p.G) * p.m_tiles_max * p.n_tiles;
   }
   if (blocks <= 0) return MOE_OK;
-  blocks = round_up(blocks, kNumXcd);
-  p.total_blocks = blocks;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, B_KCONTIG, EPI, kBM, kBN, kBK>), dim3(blocks), dim3(kThreads), 0,
+  MOE_REQUIRE(blocks < (1ll << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", name);
+  p.total_blocks = round_up(static_cast<int>(blocks), kNumXcd);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>), dim3(p.total_blocks), dim3(CFG::kThreads), 0,
                      stream, p);
   return launch_status(name);
 }
@@ -628,10 +667,9 @@ int router_logits_partials(const bf16_t* x, const bf16_t* wr, float* partials, i
   p.k_splits = splits;
   p.k_chunk = k_chunk;
   p.split_stride = static_cast<int64_t>(T) * E;
-  p.n_tiles = (E + kBN - 1) / kBN;
   int rc = set_bytes(p, static_cast<int64_t>(T) * H * 2, static_cast<int64_t>(E) * H * 2, "router logits");
   if (rc) return rc;
-  return launch<MODE_MG, true, EPI_F32>(p, stream, "router logits (split-K)");
+  return launch<MODE_MG, true, EPI_F32, SmallTile>(p, stream, "router logits (split-K)");
 }
 
 // Router weight gradient as row-chunk partials: partials[c][E][H] (f32) over
@@ -653,10 +691,27 @@ int router_wgrad_partials(const bf16_t* dl, const bf16_t* x, float* partials, in
   p.ldc = H;
   p.ldp = 1;  // f32 destination
   p.stride_cg = static_cast<int64_t>(E) * H;
-  p.n_tiles = (H + kBN - 1) / kBN;
   int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(T) * H * 2, "router wgrad");
   if (rc) return rc;
-  return launch<MODE_KG, false, EPI_WGRAD>(p, stream, "router wgrad (row chunks)");
+  return launch<MODE_KG, false, EPI_WGRAD, SmallTile>(p, stream, "router wgrad (row chunks)");
+}
+
+// Router input gradient dx[T,H] = dl[T,E] . wr[E,H] (single group, reduction E).
+int router_dgrad(const bf16_t* dl, const bf16_t* wr, bf16_t* dx, int T, int H, int E, hipStream_t stream) {
+  GemmParams p{};
+  p.A = dl;
+  p.B = wr;
+  p.C = dx;
+  p.G = 1;
+  p.rows = p.M = T;
+  p.N = H;
+  p.K = E;
+  p.lda = E;
+  p.ldb = H;
+  p.ldc = H;
+  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(E) * H * 2, "router dgrad");
+  if (rc) return rc;
+  return launch<MODE_MG, false, EPI_BF16, SmallTile>(p, stream, "router dgrad");
 }
 
 }  // namespace moe
@@ -685,11 +740,8 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
   p.ldp = 2 * I;
   p.stride_bg = 2 * I * H;
   p.swiglu_I = static_cast<int>(I);
-  p.n_tiles = static_cast<int>((2 * I + kBN - 1) / kBN);
-  // Each tile covers BN/2 act columns; the gate/up pairing needs I in whole sub-tiles.
-  p.n_tiles = static_cast<int>((I + kBN / 2 - 1) / (kBN / 2));
   if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
-  return launch<MODE_MG, true, EPI_SWIGLU_FWD>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
+  return launch<MODE_MG, true, EPI_SWIGLU_FWD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
 }
 
 extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t* offs, int64_t G, int64_t M, int64_t N,
@@ -711,33 +763,20 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
   p.ldb = K;
   p.ldc = N;
   p.stride_bg = N * K;
-  p.n_tiles = static_cast<int>((N + kBN - 1) / kBN);
   if ((rc = set_bytes(p, M * K * 2, N * K * 2, "moe_grouped_gemm_fwd"))) return rc;
-  return launch<MODE_MG, true, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_fwd");
+  return launch<MODE_MG, true, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_fwd");
 }
 
-// Router logits: f32 output, single group.
+// Router logits: f32 output, single group, no split.
 extern "C" int moe_router_logits_fwd(const void* x, const void* wr, float* logits, int64_t T, int64_t H, int64_t E,
                                      void* stream) {
   int rc = check_common(x, wr, nullptr, 1, T, E, H);
   if (rc) return rc;
   MOE_REQUIRE(logits && aligned16(logits), MOE_ERR_INVALID, "router logits: bad output pointer");
   if (T == 0) return MOE_OK;
-  GemmParams p{};
-  p.A = static_cast<const bf16_t*>(x);
-  p.B = static_cast<const bf16_t*>(wr);
-  p.C = logits;
-  p.offs = nullptr;
-  p.G = 1;
-  p.rows = p.M = static_cast<int>(T);
-  p.N = static_cast<int>(E);
-  p.K = static_cast<int>(H);
-  p.lda = H;
-  p.ldb = H;
-  p.ldc = E;
-  p.n_tiles = static_cast<int>((E + kBN - 1) / kBN);
-  if ((rc = set_bytes(p, T * H * 2, E * H * 2, "moe_router_logits_fwd"))) return rc;
-  return launch<MODE_MG, true, EPI_F32>(p, as_stream(stream), "moe_router_logits_fwd");
+  return router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), logits,
+                                static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), 1,
+                                static_cast<int>(H), as_stream(stream));
 }
 
 extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32_t* offs, int64_t G, int64_t M,
@@ -760,9 +799,8 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   p.ldb = K;
   p.ldc = K;
   p.stride_bg = N * K;
-  p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
   if ((rc = set_bytes(p, M * N * 2, N * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
-  return launch<MODE_MG, false, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
+  return launch<MODE_MG, false, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
 }
 
 extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down, const void* pre,
@@ -789,9 +827,8 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   p.ldc = 2 * I;
   p.ldp = 2 * I;
   p.stride_bg = H * I;
-  p.n_tiles = static_cast<int>((I + kBN - 1) / kBN);
   if ((rc = set_bytes(p, M * H * 2, H * I * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
-  return launch<MODE_MG, false, EPI_SWIGLU_BWD>(p, as_stream(stream), "moe_grouped_gemm_dgrad_swiglu_bwd");
+  return launch<MODE_MG, false, EPI_SWIGLU_BWD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad_swiglu_bwd");
 }
 
 extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
@@ -816,7 +853,7 @@ extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32
   p.ldp = dw_is_f32 ? 1 : 0;
   p.stride_cg = N * K;
   p.accumulate = accumulate ? 1 : 0;
-  p.n_tiles = static_cast<int>((K + kBN - 1) / kBN);
+  p.chunk_rows = static_cast<int>(M);
   if ((rc = set_bytes(p, M * N * 2, M * K * 2, "moe_grouped_gemm_wgrad"))) return rc;
-  return launch<MODE_KG, false, EPI_WGRAD>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
+  return launch<MODE_KG, false, EPI_WGRAD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
 }

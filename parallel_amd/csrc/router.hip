@@ -62,15 +62,7 @@ __device__ __forceinline__ void select_topk(const float (&v)[kMaxPerLane], int n
         bidx = e;
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      float ob = __shfl_xor(best, o, kWave);
-      int oi = __shfl_xor(bidx, o, kWave);
-      if (ob > best || (ob == best && oi < bidx)) {
-        best = ob;
-        bidx = oi;
-      }
-    }
+    wave_argmax(best, bidx);
     sel_idx[r] = bidx;
     sel_logit[r] = best;
     if (bidx != 0x7fffffff && (bidx & (kWave - 1)) == lane) taken |= 1u << (bidx / kWave);
@@ -239,10 +231,11 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
 
 // ------------------------------------------------------------------ aux loss
 
-constexpr int kAuxBlocksMax = 256;
+constexpr int kAuxBlocksMax = 1024;
+constexpr int kAuxTokensPerWave = 4;
 
 int aux_blocks(int64_t T) {
-  int64_t b = (T + 63) / 64;
+  int64_t b = (T + kRouterWaves * kAuxTokensPerWave - 1) / (kRouterWaves * kAuxTokensPerWave);
   if (b < 1) b = 1;
   return static_cast<int>(b < kAuxBlocksMax ? b : kAuxBlocksMax);
 }
@@ -537,7 +530,8 @@ extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, c
   float* partials = static_cast<float*>(workspace);
   int rc;
   if (T > 0) {  // with no tokens the reduction below writes a zero gradient
-    rc = moe_grouped_gemm_dgrad(d_logits_bf16, wr, nullptr, 1, T, E, H, dx, stream);
+    rc = router_dgrad(static_cast<const bf16_t*>(d_logits_bf16), static_cast<const bf16_t*>(wr),
+                      static_cast<bf16_t*>(dx), static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), st);
     if (rc) return rc;
     rc = router_wgrad_partials(static_cast<const bf16_t*>(d_logits_bf16), static_cast<const bf16_t*>(x), partials,
                                static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), chunks,

@@ -143,6 +143,7 @@ def _(x, weight, logits, indices, d_logits, d_scores, norm_topk_prob):
 
 
 def _router_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
     x, weight, top_k, norm, _bias = inputs
     logits, _, idx = output
     ctx.save_for_backward(x, weight, logits, idx)
@@ -203,6 +204,7 @@ def _(logits, token_weight, stats, d_aux):
 
 
 def _aux_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
     logits, token_weight, _, _ = inputs
     _, stats = output
     ctx.save_for_backward(logits, token_weight, stats)
@@ -212,6 +214,8 @@ def _aux_setup(ctx, inputs, output):
 
 def _aux_backward(ctx, d_aux, _d_stats):
     logits, token_weight, stats = ctx.saved_tensors
+    if d_aux is None:
+        return None, None, None, None
     dl = aux_loss_bwd(logits, token_weight, stats, d_aux)
     return dl.to(ctx.logits_dtype), None, None, None
 
@@ -377,6 +381,7 @@ def _(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slo
 
 
 def _experts_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
     hidden, top_k_index, top_k_weights, gate_up_proj, down_proj = inputs
     _, xp, pre, act, y, pos, offsets = output
     ctx.save_for_backward(top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos, offsets)
@@ -448,6 +453,7 @@ def _(hidden, global_indices, scores, local_count, ep_size):
 
 
 def _dispatch_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
     hidden, global_indices, scores, local_count, ep_size = inputs
     _, send_experts, _, source_tokens, pos, counts = output
     ctx.save_for_backward(pos)
@@ -508,6 +514,7 @@ def _(d_out, pos_of_slot, top_k):
 
 
 def _combine_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
     _, pos, _, top_k = inputs
     ctx.save_for_backward(pos)
     ctx.top_k = top_k
@@ -515,6 +522,8 @@ def _combine_setup(ctx, inputs, output):
 
 def _combine_backward(ctx, d_out):
     (pos,) = ctx.saved_tensors
+    if d_out is None:
+        return None, None, None, None
     return combine_rows_bwd(d_out, pos, ctx.top_k), None, None, None
 
 

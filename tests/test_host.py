@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_library_size_queries_and_argument_checks_run_without_a_gpu():
     lib = _lib.load()
     assert lib.moe_permute_workspace_bytes(32768, 128) == 16 * 129 * 4
-    assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (64 + 1) * 257 * 4
+    assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (4096 // 16 + 1) * 257 * 4
     assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) >= 4096 * 128 * 4
     # invalid sizes are rejected before any HIP call
     rc = lib.moe_grouped_gemm_fwd(None, None, None, 1, 8, 8, 8, None, None)
