@@ -8,18 +8,18 @@
 // expert), KG = groups partition the reduction (variable K per expert).
 //
 // Tiling: WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of 32x32
-// MFMA sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators in AGPRs).
-// The expert GEMMs use 256x256x64 tiles on 8 waves (two waves per SIMD, one
-// workgroup per CU, 144 KiB of LDS); the small router GEMMs use 128x128x64 on
-// 4 waves.  Operands are staged through LDS as K-contiguous rows (row stride
-// BK+8 elements) with double buffering and register prefetch of the next
-// k-tile.  Operands that are contiguous along M/N in HBM are transposed in
-// registers (8x8 bf16 blocks, v_perm) on their way into LDS so every MFMA
-// fragment read is one 16-byte ds_read.  Global reads are raw buffer loads:
-// offsets past the resource size read as zero, so ragged rows and the K tail
-// need no branches.  Sub-tiles of a wave that lie wholly outside the valid
-// rows/columns skip their fragment reads and MFMAs (the last M tile of an
-// expert is usually short).
+// MFMA sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators).  The expert
+// GEMMs use 256x256 tiles on 8 waves (two waves per SIMD, one workgroup per
+// CU); the small router GEMMs use 128x128 on 4 waves.  Operands move from HBM
+// to LDS by DMA (buffer_load_dwordx4 ... lds, no register staging) into a
+// 4-deep ring of 32-deep k-tiles, so three k-tiles of loads are in flight
+// while one is multiplied.  Each operand keeps its HBM layout in LDS (XOR
+// swizzled): K-contiguous fragments are ds_read_b128, M/N-contiguous ones
+// (weights in the input gradient, both operands of the weight gradient) are
+// ds_read_b64_tr_b16 transpose reads.  Buffer loads read zero past the
+// resource size, so ragged rows and the K tail need no branches.  Sub-tiles
+// of a wave that lie wholly outside the valid rows/columns skip their
+// fragment reads and MFMAs (the last M tile of an expert is usually short).
 //
 // Tiles are mapped to groups on the device from the `offs` cumsum (no host
 // sync).  The logical tile order is group-major, then n-tile, then m-tile, so
@@ -62,55 +62,12 @@ struct GemmParams {
 
 // ---------------------------------------------------------------- helpers
 
-__device__ __forceinline__ uint32_t sel_lo(uint32_t a, uint32_t b) {
-  // low halves: (lo16(a), lo16(b)) packed as a | b<<16
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t sel_hi(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
-// Column c (0..7) of an 8x8 bf16 block given as eight 16-byte rows (row = k),
-// returned as 8 bf16 (k = 0..7) in one 16-byte vector.
-__device__ __forceinline__ uint4 column8(const uint4* v, int c) {
-  uint32_t w[8];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    switch (c >> 1) {
-      case 0: w[q] = v[q].x; break;
-      case 1: w[q] = v[q].y; break;
-      case 2: w[q] = v[q].z; break;
-      default: w[q] = v[q].w; break;
-    }
-  }
-  uint4 r;
-  if (c & 1) {
-    r.x = sel_hi(w[0], w[1]);
-    r.y = sel_hi(w[2], w[3]);
-    r.z = sel_hi(w[4], w[5]);
-    r.w = sel_hi(w[6], w[7]);
-  } else {
-    r.x = sel_lo(w[0], w[1]);
-    r.y = sel_lo(w[2], w[3]);
-    r.z = sel_lo(w[4], w[5]);
-    r.w = sel_lo(w[6], w[7]);
-  }
-  return r;
-}
-
 // Raw buffer loads: offsets at or past the resource's byte size read as zero
 // in hardware, so out-of-range rows and the K tail need no branches.
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t kOOB = 0x80000000u;  // >= every resource size (host checks < 2 GiB)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return make_uint4(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y), static_cast<uint32_t>(v.z),
-                    static_cast<uint32_t>(v.w));
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
@@ -151,39 +108,78 @@ __device__ __forceinline__ bool locate_group(const int32_t* offs, int G, int row
   return false;
 }
 
-// Tile configurations.
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+// Tile configurations: BK-deep k-tiles staged through a STAGES-deep LDS ring.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
 struct TileCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int kThreads = 64 * WM * WN;
 };
-using BigTile = TileCfg<256, 256, 64, 2, 4>;    // expert GEMMs
-using SmallTile = TileCfg<128, 128, 64, 2, 2>;  // router GEMMs (N = E = 128)
+using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;    // expert GEMMs: 128 KiB LDS ring, 8 waves
+using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;  // router GEMMs (N = E = 128): 64 KiB ring
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 // ------------------------------------------------------------------ kernel
+//
+// LDS layouts (per stage, per operand; 16-byte chunks, XOR-swizzled so that
+// the MFMA fragment reads are free of bank conflicts on 32 banks):
+//   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ ((r >> 1) & 3)
+//   M/N-contiguous operand [BK k][R cols]: chunk c of k-row kk at slot c ^ (2 * (kk & 3))
+// Each DMA instruction (buffer_load_dwordx4 ... lds) fills one contiguous
+// 1 KiB block lane by lane (lane l -> bytes 16l..16l+15), so a lane loads
+// whichever global chunk belongs at its slot.  K-contiguous fragments are one
+// ds_read_b128; M/N-contiguous fragments are two ds_read_b64_tr_b16, which
+// turn a 4 (k) x 16 (n) patch read by 16 lanes into 4 consecutive k per lane.
 
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
 __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmParams p) {
-  constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN;
+  constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, STAGES = CFG::STAGES;
   constexpr int kThreads = CFG::kThreads;
-  constexpr int LDS_STRIDE = BK + 8;  // elements
-  constexpr int WTM = BM / WM;        // wave tile rows
-  constexpr int WTN = BN / WN;        // wave tile cols
-  constexpr int SM = WTM / 32;        // 32x32 sub-tiles per wave along M
-  constexpr int SN = WTN / 32;        // ... along N
-  constexpr bool A_KCONTIG = (MODE == MODE_MG);
-  constexpr bool BK_CONTIG = (MODE == MODE_MG) && B_KCONTIG;
-  static_assert(BK % 16 == 0, "BK must be a multiple of the MFMA K (16)");
+  constexpr int NWAVES = WM * WN;
+  constexpr int WTM = BM / WM;  // wave tile rows
+  constexpr int WTN = BN / WN;  // wave tile cols
+  constexpr int SM = WTM / 32;  // 32x32 sub-tiles per wave along M
+  constexpr int SN = WTN / 32;  // ... along N
+  constexpr bool A_KC = (MODE == MODE_MG);
+  constexpr bool B_KC = (MODE == MODE_MG) && B_KCONTIG;
+  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
+  constexpr int LPW = (NI_A + NI_B) / NWAVES;                  // ... per wave
+  static_assert(BK == 32, "swizzles and DMA mapping assume 32-deep k-tiles (4 chunks per K-contiguous row)");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 sub-tiles");
-  static_assert((BM * BK / 8) % kThreads == 0 && (BN * BK / 8) % kThreads == 0, "tile too small for loader");
+  static_assert((NI_A + NI_B) % NWAVES == 0 && NI_A % LPW == 0, "DMA instructions split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
+  static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
 
-  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LDS_STRIDE];
+  // One LDS array per ring stage: with distinct objects the compiler can tell
+  // the stage being read from the stages being filled by DMA.
+  __shared__ __attribute__((aligned(1024))) char smem0[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem1[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem2[STAGES > 2 ? STAGE_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) char smem3[STAGES > 3 ? STAGE_BYTES : 16];
+  auto stage_ptr = [&](auto st) -> char* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return smem0;
+    else if constexpr (S == 1) return smem1;
+    else if constexpr (S == 2) return smem2;
+    else return smem3;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  // Wave-uniform values live in scalar registers: buffer resources and the
+  // DMA LDS base (M0) must be uniform, or the compiler waterfalls each load.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
   // XCD-aware remap of the launch index to a logical tile index.
@@ -195,7 +191,6 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   int g, m0, n0;               // group, first output row (within group for KG), first output col
   int row_begin, row_end;      // MG: absolute activation rows of the group; KG: reduction rows
   int split = 0, k_begin = 0;  // split-K partial index and its first reduction index
-  const bf16_t* Bg = p.B;
   if constexpr (MODE == MODE_MG) {
     if (p.offs) {
       int tile0, row0, cnt;
@@ -223,7 +218,6 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       n0 = nt * BN;
       k_begin = split * p.k_chunk;
     }
-    Bg = p.B + static_cast<int64_t>(g) * p.stride_bg;
   } else {
     const int per_group = p.n_tiles * p.m_tiles_max;
     g = L / per_group;
@@ -241,6 +235,14 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     m0 = mt * BM;
     n0 = nt * BN;
   }
+  g = __builtin_amdgcn_readfirstlane(g);
+  m0 = __builtin_amdgcn_readfirstlane(m0);
+  n0 = __builtin_amdgcn_readfirstlane(n0);
+  row_begin = __builtin_amdgcn_readfirstlane(row_begin);
+  row_end = __builtin_amdgcn_readfirstlane(row_end);
+  split = __builtin_amdgcn_readfirstlane(split);
+  k_begin = __builtin_amdgcn_readfirstlane(k_begin);
+  const bf16_t* Bg = (MODE == MODE_MG) ? p.B + static_cast<int64_t>(g) * p.stride_bg : p.B;
 
   // Reduction length for this tile.
   const int Kred = (MODE == MODE_MG) ? min(p.K - k_begin, p.k_chunk) : (row_end - row_begin);
@@ -260,7 +262,9 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const int act_sm = __builtin_amdgcn_readfirstlane(min(SM, max(0, (row_limit - wrow0 + 31) / 32)));
   const int act_sn =
       __builtin_amdgcn_readfirstlane((EPI == EPI_SWIGLU_FWD) ? SN : min(SN, max(0, (p.N - wcol0 + 31) / 32)));
-  const bool full_tile = (act_sm == SM) && (act_sn == SN);
+  // Waves with no valid output rows or columns skip the MFMAs (they still
+  // take part in the DMA and the barriers).
+  const bool wave_active = act_sm > 0 && act_sn > 0;
 
   f32x16_t acc[SM][SN];
 #pragma unroll
@@ -270,222 +274,212 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // ------------------------------------------------------ loaders
-  // K-contiguous operand: 16-byte chunks, chunk c -> (row c / CH, k-chunk c % CH).
-  // M/N-contiguous operand: 8x8 blocks, block b -> (k-chunk b % CH, mn-block b / CH);
-  // the k-chunk varies fastest across lanes, which makes each global load a
-  // 128-byte run per row and the transposed 16-byte LDS stores conflict-free.
-  // A transposed operand is loaded by the first half of the threads and a
-  // transposed B by the second half.
-  constexpr int CH = BK / 8;
-  constexpr int NBA = A_KCONTIG ? 0 : CH * (BM / 8);  // 8x8 blocks of A
-  constexpr int NBB = BK_CONTIG ? 0 : CH * (BN / 8);
-  constexpr int A_TOFF = 0;
-  constexpr int B_TOFF = BK_CONTIG ? 0 : kThreads / 2;
-  constexpr int NLA = A_KCONTIG ? (BM * CH) / kThreads : (NBA + kThreads - 1) / kThreads;
-  constexpr int NLB = BK_CONTIG ? (BN * CH) / kThreads : (NBB + kThreads - 1) / kThreads;
-  static_assert(A_KCONTIG || NBA % kWave == 0, "A block count must be whole waves");
-  static_assert(BK_CONTIG || NBB % kWave == 0, "B block count must be whole waves");
-
-  // Buffer resources: A over all activation rows, B over this group's matrix.
+  // ------------------------------------------------------ DMA setup
+  // Wave w issues DMA instructions w*LPW .. w*LPW+LPW-1 of each k-tile; the
+  // first NI_A belong to A, the rest to B (a wave's instructions never span
+  // both).  Per lane and instruction: the LDS byte offset within a stage, a
+  // fixed part of the global byte offset, and the k (K-contiguous: the k
+  // chunk; M/N-contiguous: the k row) it adds per k-tile.
+  const bool dma_a = (wave * LPW) < NI_A;  // wave-uniform
   const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bg, p.b_bytes);
-
-  // Per-thread byte offsets of K-contiguous rows (fixed over k); kOOB marks
-  // rows outside the tile's valid range.
-  uint32_t a_row_off[A_KCONTIG ? NLA : 1];
-  uint32_t b_row_off[BK_CONTIG ? NLB : 1];
-
-  if constexpr (A_KCONTIG) {
+  uint32_t dma_lds[LPW];   // stage-relative LDS byte offset of this wave's instruction j
+  uint32_t dma_base[LPW];  // K-contiguous: row byte offset + chunk bytes (kOOB if the row is invalid);
+                           // M/N-contiguous: column byte offset (kOOB if the column is invalid)
+  int dma_k[LPW];          // K-contiguous: k of the chunk; M/N-contiguous: k row within the tile
 #pragma unroll
-    for (int i = 0; i < NLA; ++i) {
-      int c = tid + i * kThreads;
-      int r = c / CH;
-      int grow = m0 + r;
-      a_row_off[i] = grow < row_end ? static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u : kOOB;
-    }
-  }
-  if constexpr (BK_CONTIG) {
-#pragma unroll
-    for (int i = 0; i < NLB; ++i) {
-      int c = tid + i * kThreads;
-      int r = c / CH;
-      int wrow;
+  for (int j = 0; j < LPW; ++j) {
+    const int inst = wave * LPW + j;
+    const bool is_a = inst < NI_A;
+    const int li = is_a ? inst : inst - NI_A;  // instruction index within the operand
+    dma_lds[j] = (is_a ? 0 : A_BYTES) + li * 1024;
+    const bool kc = is_a ? A_KC : B_KC;
+    if (kc) {
+      // 16 rows x 4 chunks: lane -> row li*16 + lane/4, slot lane%4.
+      const int r = li * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      dma_k[j] = c * 8;
       bool ok;
-      if constexpr (EPI == EPI_SWIGLU_FWD) {
-        // Tile row r -> (wave column, sub-tile, half): the first SN/2 sub-tiles
-        // of each wave column are gate rows, the rest the matching up rows.
-        int wcol = r / WTN;
-        int within = r % WTN;
-        int sn = within / 32;
-        int half = sn / (SN / 2);
-        int act_col = (n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
-        ok = act_col < p.swiglu_I;
-        wrow = half * p.swiglu_I + act_col;
+      uint32_t row_bytes;
+      if (is_a) {
+        const int grow = m0 + r;
+        ok = grow < row_end;
+        row_bytes = static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u;
       } else {
-        wrow = n0 + r;
-        ok = wrow < p.N;
+        int wrow;
+        if constexpr (EPI == EPI_SWIGLU_FWD) {
+          // Tile row r -> (wave column, sub-tile, half): the first SN/2
+          // sub-tiles of each wave column are gate rows, the rest the
+          // matching up rows.
+          const int wcol = r / WTN;
+          const int within = r % WTN;
+          const int sn = within / 32;
+          const int half = sn / (SN / 2);
+          const int act_col = (n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
+          ok = act_col < p.swiglu_I;
+          wrow = half * p.swiglu_I + act_col;
+        } else {
+          wrow = n0 + r;
+          ok = wrow < p.N;
+        }
+        row_bytes = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u;
       }
-      b_row_off[i] = ok ? static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u : kOOB;
+      dma_base[j] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u : kOOB;
+    } else {
+      // k-rows of R columns: R/8 chunks per k-row, 64/(R/8) k-rows per instruction.
+      const int R = is_a ? BM : BN;
+      const int cpk = R / 8;
+      const int kk = li * (64 / cpk) + lane / cpk;
+      const int c = (lane % cpk) ^ (2 * (kk & 3));
+      const int col = (is_a ? m0 : n0) + c * 8;
+      const bool ok = col < (is_a ? p.M : p.N);
+      dma_k[j] = kk;
+      dma_base[j] = ok ? static_cast<uint32_t>(col) * 2u : kOOB;
     }
   }
+  const int mc_row0 = (MODE == MODE_KG) ? row_begin : k_begin;  // global row of tile k = 0 (M/N-contiguous)
+  const uint32_t mc_ld = static_cast<uint32_t>(dma_a ? p.lda : p.ldb) * 2u;
 
-  uint4 ra[A_KCONTIG ? NLA : NLA * 8];
-  uint4 rb[BK_CONTIG ? NLB : NLB * 8];
-
-  auto load_tile = [&](int k0) {
-    // A
-    if constexpr (A_KCONTIG) {
+  // Issue the DMA of k-tile kt into ring stage ST.  The operand a wave loads
+  // is wave-uniform: its buffer resource and offset formula are selected
+  // without branches, so every wave runs the same straight-line code.
+  auto issue_tile = [&](int kt, auto st) {
+    const int k0 = kt * BK;
+    char* stage = stage_ptr(st);
+    const __amdgpu_buffer_rsrc_t rs = dma_a ? rsA : rsB;
+    const bool kc = dma_a ? A_KC : B_KC;
 #pragma unroll
-      for (int i = 0; i < NLA; ++i) {
-        int c = tid + i * kThreads;
-        int kc = (c % CH) * 8;
-        uint32_t off = (k0 + kc) < Kred ? a_row_off[i] + static_cast<uint32_t>(k_begin + k0 + kc) * 2u : kOOB;
-        ra[i] = bload16(rsA, off);
-      }
-    } else {
-      // A is M-contiguous: tile = BK reduction rows x BM columns, 8x8 blocks.
-#pragma unroll
-      for (int i = 0; i < NLA; ++i) {
-        int blk = ((tid + A_TOFF) % kThreads) + i * kThreads;
-        if (blk < NBA) {
-          int kc = blk % CH, mb = blk / CH;
-          int col = m0 + mb * 8;
-          bool col_ok = col < p.M;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            int kk = k0 + kc * 8 + q;
-            bool ok = col_ok && kk < Kred;
-            uint32_t off = ok ? (static_cast<uint32_t>(row_begin + kk) * static_cast<uint32_t>(p.lda) +
-                                 static_cast<uint32_t>(col)) * 2u
-                              : kOOB;
-            ra[i * 8 + q] = bload16(rsA, off);
-          }
-        }
-      }
-    }
-    // B
-    if constexpr (BK_CONTIG) {
-#pragma unroll
-      for (int i = 0; i < NLB; ++i) {
-        int c = tid + i * kThreads;
-        int kc = (c % CH) * 8;
-        uint32_t off = (k0 + kc) < Kred ? b_row_off[i] + static_cast<uint32_t>(k_begin + k0 + kc) * 2u : kOOB;
-        rb[i] = bload16(rsB, off);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < NLB; ++i) {
-        int blk = ((tid + B_TOFF) % kThreads) + i * kThreads;
-        if (blk < NBB) {
-          int kc = blk % CH, nb8 = blk / CH;
-          int col = n0 + nb8 * 8;
-          bool col_ok = col < p.N;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            int kk = k0 + kc * 8 + q;
-            bool ok = col_ok && kk < Kred;
-            int rowi = (MODE == MODE_KG) ? row_begin + kk : k_begin + kk;
-            uint32_t off = ok ? (static_cast<uint32_t>(rowi) * static_cast<uint32_t>(p.ldb) +
-                                 static_cast<uint32_t>(col)) * 2u
-                              : kOOB;
-            rb[i * 8 + q] = bload16(rsB, off);
-          }
-        }
-      }
+    for (int j = 0; j < LPW; ++j) {
+      const int kk = k0 + dma_k[j];  // K-contiguous: k of the chunk; M/N-contiguous: k row
+      const uint32_t kc_off = dma_base[j] + static_cast<uint32_t>(k_begin + k0) * 2u;
+      const uint32_t mc_off = static_cast<uint32_t>(mc_row0 + kk) * mc_ld + dma_base[j];
+      const uint32_t off = (kk < Kred && dma_base[j] != kOOB) ? (kc ? kc_off : mc_off) : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(stage + dma_lds[j]), 16, off, 0, 0, 0);
     }
   };
 
-  auto store_tile = [&](int buf) {
-    bf16_t* as = As[buf];
-    bf16_t* bs = Bs[buf];
-    if constexpr (A_KCONTIG) {
+  // ------------------------------------------------------ fragment reads
+  // Each lane's byte offset within a stage is precomputed per fragment
+  // class, so every fragment address is the stage array plus one lane
+  // offset plus a constant.  Short address chains keep the per-stage alias
+  // scopes that the compiler attaches to LDS accesses (it follows only a few
+  // levels of address arithmetic); without them a fragment read waits for
+  // every DMA in flight.
+  const int l32 = lane & 31;
+  const int khalf = lane >> 5;
+  // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk 2 ks + khalf.
+  const int kc_swz = (l32 >> 1) & 3;
+  int a_kc[2], b_kc[2];
 #pragma unroll
-      for (int i = 0; i < NLA; ++i) {
-        int c = tid + i * kThreads;
-        int r = c / CH, kc = (c % CH) * 8;
-        *reinterpret_cast<uint4*>(as + r * LDS_STRIDE + kc) = ra[i];
-      }
-    } else {
+  for (int ks = 0; ks < 2; ++ks) {
+    const int lane_off = l32 * 64 + (((2 * ks + khalf) ^ kc_swz) << 4);
+    a_kc[ks] = wm * WTM * 64 + lane_off;
+    b_kc[ks] = A_BYTES + wn * WTN * 64 + lane_off;
+  }
+  // M/N-contiguous [BK k-rows][R cols] (transpose reads): lane = 16 q + i reads
+  // k-rows 16 ks + 8 (q/2) + 4 h + i/4 and columns tile_col + 16 (q%2) + 4 (i%4).
+  // The slot swizzle XORs chunk bits 1-2, so the offset depends on the
+  // parity of the 32-column sub-tile within its 64-column group; wave tiles
+  // start on 64-column boundaries.
+  static_assert(A_KC || WTM % 64 == 0, "transpose-read offsets assume 64-column wave tiles");
+  static_assert(B_KC || WTN % 64 == 0, "transpose-read offsets assume 64-column wave tiles");
+  const int q16 = lane >> 4, i16 = lane & 15;
+  const int tr_krow = 8 * (q16 >> 1) + (i16 >> 2);
+  const int tr_col = 16 * (q16 & 1) + 4 * (i16 & 3);
+  const int tr_swz = 2 * ((i16 >> 2) & 3);  // 2 * (k-row & 3)
+  int a_mc[2], b_mc[2];
 #pragma unroll
-      for (int i = 0; i < NLA; ++i) {
-        int blk = ((tid + A_TOFF) % kThreads) + i * kThreads;
-        if (blk < NBA) {
-          int kc = blk % CH, mb = blk / CH;
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            *reinterpret_cast<uint4*>(as + (mb * 8 + c) * LDS_STRIDE + kc * 8) = column8(ra + i * 8, c);
-        }
-      }
-    }
-    if constexpr (BK_CONTIG) {
-#pragma unroll
-      for (int i = 0; i < NLB; ++i) {
-        int c = tid + i * kThreads;
-        int r = c / CH, kc = (c % CH) * 8;
-        *reinterpret_cast<uint4*>(bs + r * LDS_STRIDE + kc) = rb[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < NLB; ++i) {
-        int blk = ((tid + B_TOFF) % kThreads) + i * kThreads;
-        if (blk < NBB) {
-          int kc = blk % CH, nb8 = blk / CH;
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            *reinterpret_cast<uint4*>(bs + (nb8 * 8 + c) * LDS_STRIDE + kc * 8) = column8(rb + i * 8, c);
-        }
-      }
-    }
+  for (int par = 0; par < 2; ++par) {
+    const int slot_lo = ((4 * par + (tr_col >> 3)) ^ tr_swz) << 4;  // low 3 chunk bits, swizzled
+    const int half8 = ((tr_col >> 2) & 1) << 3;
+    a_mc[par] = tr_krow * BM * 2 + ((wm * WTM) >> 3) * 16 + slot_lo + half8;
+    b_mc[par] = A_BYTES + tr_krow * BN * 2 + ((wn * WTN) >> 3) * 16 + slot_lo + half8;
+  }
+
+  auto ld_frag_kc = [&](const char* stage, int lane_off, int row0_const) -> bf16x8_t {
+    return *reinterpret_cast<const bf16x8_t*>(stage + lane_off + row0_const * 64);
+  };
+  // Sub-tile t (32 columns) of a wave tile with R columns per k-row.
+  auto ld_frag_mc = [&](const char* stage, const int* lane_off, int R, int t, int ks) -> bf16x8_t {
+    const char* p = stage + lane_off[t & 1] + (t & ~1) * 64 + 16 * ks * R * 2;
+    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
+    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * R * 2));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8_t, v);
   };
 
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
-
-  // FULL: every sub-tile active, no control flow between the fragment reads
-  // and the MFMAs; otherwise skip the inactive sub-tiles (uniform branches).
-  auto compute_tile = [&](int buf, auto full) {
-    constexpr bool FULL = decltype(full)::value;
-    const bf16_t* as = As[buf] + (wm * WTM + frag_row) * LDS_STRIDE + frag_k;
-    const bf16_t* bs = Bs[buf] + (wn * WTN + frag_row) * LDS_STRIDE + frag_k;
+  auto compute_tile = [&](auto st) {
+    const char* stage = stage_ptr(st);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[SM], bfr[SN];
 #pragma unroll
       for (int i = 0; i < SM; ++i)
-        if (FULL || i < act_sm) af[i] = *reinterpret_cast<const bf16x8_t*>(as + i * 32 * LDS_STRIDE + ks * 16);
+        af[i] = A_KC ? ld_frag_kc(stage, a_kc[ks], i * 32) : ld_frag_mc(stage, a_mc, BM, i, ks);
 #pragma unroll
       for (int j = 0; j < SN; ++j)
-        if (FULL || j < act_sn) bfr[j] = *reinterpret_cast<const bf16x8_t*>(bs + j * 32 * LDS_STRIDE + ks * 16);
+        bfr[j] = B_KC ? ld_frag_kc(stage, b_kc[ks], j * 32) : ld_frag_mc(stage, b_mc, BN, j, ks);
 #pragma unroll
       for (int i = 0; i < SM; ++i)
 #pragma unroll
         for (int j = 0; j < SN; ++j)
           // Operands swapped: the result holds C^T fragments, so each lane
           // owns one output row and runs of 4 consecutive output columns.
-          if (FULL || (i < act_sm && j < act_sn))
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     }
   };
 
-  auto main_loop = [&](auto full) {
-    const int nk = (Kred + BK - 1) / BK;
-    if (nk <= 0) return;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load_tile((kt + 1) * BK);
-      compute_tile(cur, full);
-      if (kt + 1 < nk) store_tile(cur ^ 1);
-      __syncthreads();
-    }
+  // Workgroup barrier without a memory fence: a fenced barrier would make the
+  // compiler drain every outstanding DMA (vmcnt(0)) each k-tile.  The empty
+  // asm statements keep LDS accesses from moving across it; the DMA of the
+  // tile about to be read is waited for explicitly with vmcnt.
+  auto barrier = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
-  if (full_tile)
-    main_loop(std::true_type{});
-  else
-    main_loop(std::false_type{});
+
+  // STAGES-deep ring: k-tile kt lives in stage kt % STAGES; the DMA of tile
+  // kt + STAGES - 1 is issued right after the barrier that retires tile
+  // kt - 1.  Every step issues exactly LPW DMA instructions per wave (past
+  // the last tile they are all out of range and only write zeros to a stage
+  // that is never read), so the wait for tile kt is always the same vmcnt.
+  //
+  // The steady-state loop runs whole groups of STAGES steps with no per-step
+  // guard, so every stage index is a compile-time constant and the
+  // compiler's LDS-DMA wait tracking (one alias scope per stage array) stays
+  // exact across the back edge: a fragment read waits only for the DMA of
+  // its own stage, which the explicit vmcnt above already retired.  Guarded
+  // steps inside the loop would merge paths with different DMA histories at
+  // the back edge and make the compiler drain every DMA (vmcnt(0)) before
+  // each step's reads.  The last nk % STAGES steps run after the loop.
+  const int nk = (Kred + BK - 1) / BK;
+  auto step = [&](int kt, auto st) {
+    constexpr int S = decltype(st)::value;
+    wait_vmcnt<(STAGES - 2) * LPW>();
+    barrier();
+    issue_tile(kt + STAGES - 1, std::integral_constant<int, (S + STAGES - 1) % STAGES>{});
+    if (wave_active) compute_tile(st);
+  };
+  if (nk > 0) {
+    issue_tile(0, std::integral_constant<int, 0>{});
+    if constexpr (STAGES > 2) issue_tile(1, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 3) issue_tile(2, std::integral_constant<int, 2 % STAGES>{});
+    int kt = 0;
+    for (; kt + STAGES <= nk; kt += STAGES) {
+      step(kt, std::integral_constant<int, 0>{});
+      step(kt + 1, std::integral_constant<int, 1>{});
+      if constexpr (STAGES > 2) step(kt + 2, std::integral_constant<int, 2 % STAGES>{});
+      if constexpr (STAGES > 3) step(kt + 3, std::integral_constant<int, 3 % STAGES>{});
+    }
+    if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+    if constexpr (STAGES > 2)
+      if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 3)
+      if (kt + 2 < nk) step(kt + 2, std::integral_constant<int, 2 % STAGES>{});
+    wait_vmcnt<0>();  // retire the trailing out-of-range DMA before the LDS is released
+  }
 
   // ------------------------------------------------------ epilogue
   // Lane owns output row  wrow0 + i*32 + (lane & 31)  and columns
