@@ -108,6 +108,24 @@ __device__ __forceinline__ bool locate_group(const int32_t* offs, int G, int row
   return false;
 }
 
+// Total tiles over all groups, sum_g n_mult * ceil(cnt_g / BM) (wave-uniform).
+template <int BM>
+__device__ __forceinline__ int count_tiles(const int32_t* offs, int G, int rows, int n_mult) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int total = 0;
+  for (int c0 = 0; c0 < G; c0 += kWave) {
+    int g = c0 + lane;
+    int nt = 0;
+    if (g < G) {
+      int hi = min(max(offs[g], 0), rows);
+      int lo = g ? min(max(offs[g - 1], 0), hi) : 0;
+      nt = n_mult * ((hi - lo + BM - 1) / BM);
+    }
+    total += __builtin_amdgcn_readlane(wave_inclusive_scan(nt), kWave - 1);
+  }
+  return __builtin_amdgcn_readfirstlane(total);
+}
+
 // Tile configurations: BK-deep k-tiles staged through a STAGES-deep LDS ring.
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
 struct TileCfg {
@@ -124,6 +142,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. N-1 (compile-time unrolled).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -131,14 +159,23 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // ------------------------------------------------------------------ kernel
 //
 // LDS layouts (per stage, per operand; 16-byte chunks, XOR-swizzled so that
-// the MFMA fragment reads are free of bank conflicts on 32 banks):
-//   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ ((r >> 1) & 3)
-//   M/N-contiguous operand [BK k][R cols]: chunk c of k-row kk at slot c ^ (2 * (kk & 3))
+// the MFMA fragment reads are free of bank conflicts: gfx950 LDS serves
+// 256 bytes per clock, so the 16 lanes of a ds_read_b128 pass, or the 32
+// lanes of a ds_read_b64_tr_b16 pass, must touch 64 distinct banks):
+//   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ kc_swizzle(r)
+//   M/N-contiguous operand [BK k][R cols]: chunk c of k-row kk at slot c ^ mc_swizzle(kk)
 // Each DMA instruction (buffer_load_dwordx4 ... lds) fills one contiguous
 // 1 KiB block lane by lane (lane l -> bytes 16l..16l+15), so a lane loads
 // whichever global chunk belongs at its slot.  K-contiguous fragments are one
 // ds_read_b128; M/N-contiguous fragments are two ds_read_b64_tr_b16, which
 // turn a 4 (k) x 16 (n) patch read by 16 lanes into 4 consecutive k per lane.
+
+// A ds_read_b128 pass reads one chunk of 16 consecutive rows: rows r and
+// r + 4k differ in bits 2-3, which move the chunk to another 16-byte bank group.
+__device__ __forceinline__ constexpr int kc_swizzle(int r) { return (r >> 2) & 3; }
+// A transpose-read pass reads 32 columns (4 chunks) of 4 consecutive k-rows:
+// k-row kk & 3 selects the 64-byte bank quarter (needs >= 16 chunks per k-row).
+__device__ __forceinline__ constexpr int mc_swizzle(int kk) { return 4 * (kk & 3); }
 
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
 __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmParams p) {
@@ -159,7 +196,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 sub-tiles");
   static_assert((NI_A + NI_B) % NWAVES == 0 && NI_A % LPW == 0, "DMA instructions split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
-  static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+  static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
 
   // One LDS array per ring stage: with distinct objects the compiler can tell
   // the stage being read from the stages being filled by DMA.
@@ -167,12 +204,14 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   __shared__ __attribute__((aligned(1024))) char smem1[STAGE_BYTES];
   __shared__ __attribute__((aligned(1024))) char smem2[STAGES > 2 ? STAGE_BYTES : 16];
   __shared__ __attribute__((aligned(1024))) char smem3[STAGES > 3 ? STAGE_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) char smem4[STAGES > 4 ? STAGE_BYTES : 16];
   auto stage_ptr = [&](auto st) -> char* {
     constexpr int S = decltype(st)::value;
     if constexpr (S == 0) return smem0;
     else if constexpr (S == 1) return smem1;
     else if constexpr (S == 2) return smem2;
-    else return smem3;
+    else if constexpr (S == 3) return smem3;
+    else return smem4;
   };
 
   const int tid = threadIdx.x;
@@ -182,10 +221,23 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
-  // XCD-aware remap of the launch index to a logical tile index.
-  const int nb = p.total_blocks;  // multiple of kNumXcd
+  // XCD-aware remap of the launch index to a logical tile index: blocks are
+  // dealt round-robin over the XCDs, so XCD x runs launch indices x, x + 8, ...;
+  // it gets the x-th contiguous share of the logical tiles.  With groups the
+  // grid is sized for the worst case, so the real tile count is computed here
+  // from `offs` and the shares are cut from it (otherwise the XCDs holding the
+  // upper end of the range would get no work).
   const int bid = blockIdx.x;
-  const int L = (bid % kNumXcd) * (nb / kNumXcd) + bid / kNumXcd;
+  const int xcd = bid % kNumXcd, xcd_idx = bid / kNumXcd;
+  int L;
+  if (MODE == MODE_MG && p.offs) {
+    const int real = count_tiles<BM>(p.offs, p.G, p.rows, p.n_tiles);
+    const int share = (real + kNumXcd - 1) / kNumXcd;
+    L = xcd * share + xcd_idx;
+    if (xcd_idx >= share || L >= real) return;
+  } else {
+    L = xcd * (p.total_blocks / kNumXcd) + xcd_idx;  // total_blocks is a multiple of kNumXcd
+  }
 
   // ------------------------------------------------------ tile -> work
   int g, m0, n0;               // group, first output row (within group for KG), first output col
@@ -297,7 +349,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     if (kc) {
       // 16 rows x 4 chunks: lane -> row li*16 + lane/4, slot lane%4.
       const int r = li * 16 + (lane >> 2);
-      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      const int c = (lane & 3) ^ kc_swizzle(r);
       dma_k[j] = c * 8;
       bool ok;
       uint32_t row_bytes;
@@ -330,7 +382,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       const int R = is_a ? BM : BN;
       const int cpk = R / 8;
       const int kk = li * (64 / cpk) + lane / cpk;
-      const int c = (lane % cpk) ^ (2 * (kk & 3));
+      const int c = (lane % cpk) ^ mc_swizzle(kk);
       const int col = (is_a ? m0 : n0) + c * 8;
       const bool ok = col < (is_a ? p.M : p.N);
       dma_k[j] = kk;
@@ -368,40 +420,38 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const int l32 = lane & 31;
   const int khalf = lane >> 5;
   // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk 2 ks + khalf.
-  const int kc_swz = (l32 >> 1) & 3;
+  // Fragment rows start on 32-row boundaries, so row & 15 == l32 & 15.
   int a_kc[2], b_kc[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int lane_off = l32 * 64 + (((2 * ks + khalf) ^ kc_swz) << 4);
+    const int lane_off = l32 * 64 + (((2 * ks + khalf) ^ kc_swizzle(l32)) << 4);
     a_kc[ks] = wm * WTM * 64 + lane_off;
     b_kc[ks] = A_BYTES + wn * WTN * 64 + lane_off;
   }
   // M/N-contiguous [BK k-rows][R cols] (transpose reads): lane = 16 q + i reads
   // k-rows 16 ks + 8 (q/2) + 4 h + i/4 and columns tile_col + 16 (q%2) + 4 (i%4).
-  // The slot swizzle XORs chunk bits 1-2, so the offset depends on the
-  // parity of the 32-column sub-tile within its 64-column group; wave tiles
-  // start on 64-column boundaries.
-  static_assert(A_KC || WTM % 64 == 0, "transpose-read offsets assume 64-column wave tiles");
-  static_assert(B_KC || WTN % 64 == 0, "transpose-read offsets assume 64-column wave tiles");
+  // The swizzle depends only on k-row & 3 == i/4, so each 32-column sub-tile
+  // has one lane offset; ks and h add constants.
+  static_assert(A_KC || BM >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
+  static_assert(B_KC || BN >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
   const int q16 = lane >> 4, i16 = lane & 15;
   const int tr_krow = 8 * (q16 >> 1) + (i16 >> 2);
   const int tr_col = 16 * (q16 & 1) + 4 * (i16 & 3);
-  const int tr_swz = 2 * ((i16 >> 2) & 3);  // 2 * (k-row & 3)
-  int a_mc[2], b_mc[2];
+  const int half8 = ((tr_col >> 2) & 1) << 3;
+  int a_mc[SM], b_mc[SN];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int slot_lo = ((4 * par + (tr_col >> 3)) ^ tr_swz) << 4;  // low 3 chunk bits, swizzled
-    const int half8 = ((tr_col >> 2) & 1) << 3;
-    a_mc[par] = tr_krow * BM * 2 + ((wm * WTM) >> 3) * 16 + slot_lo + half8;
-    b_mc[par] = A_BYTES + tr_krow * BN * 2 + ((wn * WTN) >> 3) * 16 + slot_lo + half8;
-  }
+  for (int t = 0; t < SM; ++t)
+    a_mc[t] = tr_krow * BM * 2 + ((((wm * WTM + 32 * t + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
+#pragma unroll
+  for (int t = 0; t < SN; ++t)
+    b_mc[t] = A_BYTES + tr_krow * BN * 2 + ((((wn * WTN + 32 * t + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
 
   auto ld_frag_kc = [&](const char* stage, int lane_off, int row0_const) -> bf16x8_t {
     return *reinterpret_cast<const bf16x8_t*>(stage + lane_off + row0_const * 64);
   };
   // Sub-tile t (32 columns) of a wave tile with R columns per k-row.
   auto ld_frag_mc = [&](const char* stage, const int* lane_off, int R, int t, int ks) -> bf16x8_t {
-    const char* p = stage + lane_off[t & 1] + (t & ~1) * 64 + 16 * ks * R * 2;
+    const char* p = stage + lane_off[t] + 16 * ks * R * 2;
     i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
     i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * R * 2));
     typedef short i16x8_t __attribute__((ext_vector_type(8)));
@@ -463,21 +513,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     if (wave_active) compute_tile(st);
   };
   if (nk > 0) {
-    issue_tile(0, std::integral_constant<int, 0>{});
-    if constexpr (STAGES > 2) issue_tile(1, std::integral_constant<int, 1>{});
-    if constexpr (STAGES > 3) issue_tile(2, std::integral_constant<int, 2 % STAGES>{});
+    static_for<STAGES - 1>([&](auto i) { issue_tile(i, i); });
     int kt = 0;
-    for (; kt + STAGES <= nk; kt += STAGES) {
-      step(kt, std::integral_constant<int, 0>{});
-      step(kt + 1, std::integral_constant<int, 1>{});
-      if constexpr (STAGES > 2) step(kt + 2, std::integral_constant<int, 2 % STAGES>{});
-      if constexpr (STAGES > 3) step(kt + 3, std::integral_constant<int, 3 % STAGES>{});
-    }
-    if (kt < nk) step(kt, std::integral_constant<int, 0>{});
-    if constexpr (STAGES > 2)
-      if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
-    if constexpr (STAGES > 3)
-      if (kt + 2 < nk) step(kt + 2, std::integral_constant<int, 2 % STAGES>{});
+    for (; kt + STAGES <= nk; kt += STAGES) static_for<STAGES>([&](auto i) { step(kt + i, i); });
+    static_for<STAGES - 1>([&](auto i) {
+      if (kt + i < nk) step(kt + i, i);
+    });
     wait_vmcnt<0>();  // retire the trailing out-of-range DMA before the LDS is released
   }
 
