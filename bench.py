@@ -34,27 +34,40 @@ def log(*a):
 
 
 def kernel_work(w, T: int, S: int):
-    """Algorithmic work per launch: ('mfma', FLOP) or ('hbm', bytes), per timer tag."""
+    """Algorithmic work per launch, per timer tag: (flops or None, bytes).
+
+    Bytes are the HBM traffic of an ideal kernel: every operand read once and
+    every output written once (bf16 activations and weights, fp32 router
+    logits and scores).  A kernel's bound is whichever of flops / MFMA peak and
+    bytes / HBM peak is larger."""
     H, I, E, k = w.hidden, w.intermediate, w.experts, w.top_k
     b = 2  # bf16
+    Wgu, Wdn = E * 2 * I * H * b, E * H * I * b  # expert weights
+    xp, act, pre, y = S * H * b, S * I * b, S * 2 * I * b, S * H * b  # permuted rows, SwiGLU act, gate|up, down out
     return {
-        "up_fwd": ("mfma", 4.0 * S * H * I),
-        "down_fwd": ("mfma", 2.0 * S * H * I),
-        "down_dgrad": ("mfma", 2.0 * S * H * I),
-        "down_wgrad": ("mfma", 2.0 * S * H * I),
-        "up_dgrad": ("mfma", 4.0 * S * H * I),
-        "up_wgrad": ("mfma", 4.0 * S * H * I),
-        "router_fwd": ("mfma", 2.0 * T * H * E),
-        "router_gemm_bwd": ("mfma", 4.0 * T * H * E),
-        # bytes: read x rows once per route and ids, write permuted rows and maps
-        "permute_fwd": ("hbm", T * H * b + S * H * b + 16.0 * S),
-        "combine_fwd": ("hbm", S * H * b + 8.0 * S + T * H * b),
-        "combine_bwd": ("hbm", T * H * b + 2.0 * S * H * b + 12.0 * S),
-        "permute_bwd": ("hbm", S * H * b + T * H * b + 4.0 * S),
-        "router_topk_bwd": ("hbm", 8.0 * T * E + 2.0 * T * E + 16.0 * T * k),
-        "aux_fwd": ("hbm", 4.0 * T * E),
-        "aux_bwd": ("hbm", 8.0 * T * E),
+        "up_fwd": (4.0 * S * H * I, xp + Wgu + act + pre),
+        "down_fwd": (2.0 * S * H * I, act + Wdn + y),
+        "down_dgrad": (2.0 * S * H * I, y + Wdn + pre + pre),
+        "down_wgrad": (2.0 * S * H * I, y + act + Wdn),
+        "up_dgrad": (4.0 * S * H * I, pre + Wgu + xp),
+        "up_wgrad": (4.0 * S * H * I, pre + xp + Wgu),
+        "router_fwd": (2.0 * T * H * E, T * H * b + E * H * b + 8.0 * T * E + 12.0 * T * k),
+        "router_gemm_bwd": (4.0 * T * H * E, T * E * b + T * H * b + E * H * b + T * H * b + 4.0 * E * H),
+        # read x rows once per route and the routes, write permuted rows and maps
+        "permute_fwd": (None, T * H * b + S * H * b + 16.0 * S),
+        "combine_fwd": (None, S * H * b + 8.0 * S + T * H * b),
+        "combine_bwd": (None, T * H * b + 2.0 * S * H * b + 12.0 * S),
+        "permute_bwd": (None, S * H * b + T * H * b + 4.0 * S),
+        "router_topk_bwd": (None, 8.0 * T * E + 2.0 * T * E + 16.0 * T * k),
+        "aux_fwd": (None, 4.0 * T * E),
+        "aux_bwd": (None, 8.0 * T * E),
     }
+
+
+def bound_of(flops, nbytes):
+    if flops is not None and flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9):
+        return "mfma"
+    return "hbm"
 
 
 def read_traffic(tag: str, workload: str):
@@ -66,6 +79,169 @@ def read_traffic(tag: str, workload: str):
         if line.startswith("hbm_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+# Kernels launched by each timed entry point (tag), matched on demangled names.
+_TAG_KERNELS = {
+    "router_reduce_topk_kernel": "router_fwd",
+    "reduce_partials_bf16_kernel": "router_gemm_bwd",
+    "router_topk_bwd_kernel": "router_topk_bwd",
+    "aux_partial_kernel": "aux_fwd",
+    "aux_reduce_kernel": "aux_fwd",
+    "aux_finalize_kernel": "aux_fwd",
+    "aux_bwd_kernel": "aux_bwd",
+    "permute_count_kernel": "permute_fwd",
+    "permute_scan_kernel": "permute_fwd",
+    "permute_scatter_kernel": "permute_fwd",
+    "gather_rows_kernel": "permute_fwd",
+    "combine_fwd_kernel": "combine_fwd",
+    "combine_bwd_kernel": "combine_bwd",
+    "permute_bwd_kernel": "permute_bwd",
+}
+_GEMM_RE = r"grouped_gemm_kernel<(\d), (true|false), (\d), moe::TileCfg<([0-9, ]+)>"
+
+
+def tag_kernels(rows):
+    """Maps (kernel name, grid size) -> bench timer tag for the library's kernels.
+
+    The expert GEMMs are the grouped_gemm instantiations sharing the tile
+    configuration of the SwiGLU forward (epilogue 2); the weight-gradient
+    instantiation serves both projections, told apart by grid size (the up
+    projection has twice the output tiles)."""
+    import re
+
+    gemm = {}
+    for name, grid in rows:
+        m = re.search(_GEMM_RE, name)
+        if m:
+            gemm[(name, grid)] = (int(m[1]), m[2] == "true", int(m[3]), m[4])
+    expert_cfg = next((v[3] for v in gemm.values() if v[2] == 2), None)
+    wgrad_grids = sorted({g for (n, g), v in gemm.items() if v[3] == expert_cfg and v[0] == 1})
+    out = {}
+    for name, grid in rows:
+        if (name, grid) in gemm:
+            mode, bkc, epi, cfg = gemm[(name, grid)]
+            if cfg == expert_cfg:
+                if mode == 1:
+                    out[(name, grid)] = "up_wgrad" if grid == wgrad_grids[-1] else "down_wgrad"
+                else:
+                    out[(name, grid)] = {(True, 2): "up_fwd", (True, 0): "down_fwd", (False, 3): "down_dgrad",
+                                         (False, 0): "up_dgrad"}.get((bkc, epi))
+            else:
+                out[(name, grid)] = "router_fwd" if (mode, bkc) == (0, True) else "router_gemm_bwd"
+            continue
+        out[(name, grid)] = next((t for k, t in _TAG_KERNELS.items() if f"moe::{k}" in name), None)
+    return out
+
+
+def _read_csvs(d):
+    import csv
+
+    rows = []
+    for f in sorted(Path(d).rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            rows.extend(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    return rows
+
+
+def profile_summary(args) -> int:
+    """Writes profiles/ summaries from rocprofv3 outputs of this script.
+
+    Kernel durations come from a --kernel-trace --stats run; HBM bytes per
+    launch from one --pmc FETCH_SIZE and one --pmc WRITE_SIZE run, each scaled
+    by what the same counter reads for a 1 GiB device copy (--copy-calibration).
+    """
+    import csv
+    from collections import defaultdict
+
+    from parallel_amd.workloads import WORKLOADS
+
+    w = WORKLOADS[args.config]
+    prof = ROOT / "profiles"
+    prof.mkdir(exist_ok=True)
+    cmd = args.profile_commands or ""
+
+    # ---- kernel durations (per dispatch, from the --kernel-trace CSV of the --stats run)
+    with open(args.trace_csv) as fh:
+        trace = list(csv.DictReader(fh))
+    disp = defaultdict(list)
+    for r in trace:
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        disp[(r["Kernel_Name"], grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    tags = tag_kernels(list(disp))
+    grand = sum(sum(v) for v in disp.values())
+    lines = [f"# rocprofv3 kernel statistics, workload {w.name} ({args.steps_profiled} timed + warm-up steps)",
+             f"# command: {cmd.splitlines()[0] if cmd else '(not recorded)'}",
+             f"# {'tag':16s} {'calls':>6s} {'avg_us':>10s} {'total_us':>11s} {'pct':>6s}  kernel [grid threads]"]
+    per_tag = defaultdict(lambda: [0.0, 0])
+    for key, ds in sorted(disp.items(), key=lambda kv: -sum(kv[1])):
+        tag = tags.get(key) or "-"
+        total = sum(ds)
+        short = key[0].replace("moe::", "").split("(")[0][:100]
+        lines.append(f"  {tag:16s} {len(ds):6d} {total / len(ds):10.1f} {total:11.1f} {100 * total / grand:6.2f}  "
+                     f"{short} [{key[1]}]")
+        if tag != "-":
+            per_tag[tag][0] += total
+            per_tag[tag][1] = max(per_tag[tag][1], len(ds))
+    lines.append("# per entry point (sum of its kernels / calls):")
+    for tag, (total, calls) in sorted(per_tag.items(), key=lambda kv: -kv[1][0]):
+        lines.append(f"avg_us_per_call {tag}: {total / calls:.1f}")
+    (prof / f"kernel_stats_{w.name}.txt").write_text("\n".join(lines) + "\n")
+
+    # ---- HBM traffic
+    def per_kernel(d, counter):
+        acc = defaultdict(list)
+        for r in _read_csvs(d):
+            if r["Counter_Name"] == counter:
+                acc[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+        return acc
+
+    def cal_factor(d, counter, expect_kib):
+        vals = [v for (n, g), vs in per_kernel(d, counter).items() if "copyBuffer" in n for v in vs]
+        if not vals:
+            raise SystemExit(f"calibration run {d} holds no copy kernel")
+        return expect_kib / statistics.fmean(vals), statistics.fmean(vals)
+
+    f_fac, f_cal = cal_factor(args.cal_fetch, "FETCH_SIZE", 1 << 20)
+    w_fac, w_cal = cal_factor(args.cal_write, "WRITE_SIZE", 1 << 20)
+    fetch = per_kernel(args.pmc_fetch, "FETCH_SIZE")
+    write = per_kernel(args.pmc_write, "WRITE_SIZE")
+    ktags = tag_kernels(list(fetch))
+    work = kernel_work(w, w.tokens, w.slots)
+    by_tag = defaultdict(lambda: {"fetch": 0.0, "write": 0.0, "kernels": set()})
+    for key, vals in fetch.items():
+        tag = ktags.get(key)
+        if tag:
+            by_tag[tag]["fetch"] += sum(vals)
+            by_tag[tag]["write"] += sum(write.get(key, []))
+            by_tag[tag]["kernels"].add(key[0].replace("moe::", "").split("(")[0])
+    for tag, d in by_tag.items():
+        calls = args.pmc_calls
+        rd = d["fetch"] / calls * f_fac * 1024
+        wr = d["write"] / calls * w_fac * 1024
+        flops, amount = work[tag]
+        body = [
+            f"# HBM traffic per launch of entry point '{tag}', workload {w.name}",
+            "# kernels: " + "; ".join(sorted(d["kernels"])),
+            "# commands (one counter per pass; calibration = 1 GiB device copy):",
+            *[f"#   {c}" for c in cmd.splitlines()],
+            f"# calibration: copy of 1 GiB reads FETCH_SIZE {f_cal:.1f} KiB (factor {f_fac:.3f}), "
+            f"writes WRITE_SIZE {w_cal:.1f} KiB (factor {w_fac:.3f})",
+            f"launches_profiled: {calls}",
+            f"fetch_size_kib_per_launch: {d['fetch'] / calls:.1f}",
+            f"write_size_kib_per_launch: {d['write'] / calls:.1f}",
+            f"read_bytes_per_launch: {rd:.0f}",
+            f"write_bytes_per_launch: {wr:.0f}",
+            f"hbm_bytes_per_launch: {rd + wr:.0f}",
+            f"algorithmic_bytes_per_launch: {amount:.0f}",
+            f"algorithmic_flops_per_launch: {flops:.0f}" if flops is not None else "algorithmic_flops_per_launch: -",
+            f"bound: {bound_of(flops, amount)}",
+        ]
+        (prof / f"{tag}_{w.name}_pmc.txt").write_text("\n".join(body) + "\n")
+    log(f"wrote {len(by_tag)} traffic summaries and kernel_stats_{w.name}.txt under {prof}")
+    return 0
 
 
 def cpu_baseline(w, tokens: int):
@@ -102,11 +278,24 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", help="workload key (c2 c3 c4 c5); c2 is the headline")
-    ap.add_argument("--cpu-baseline-tokens", type=int, default=1024)
+    ap.add_argument("--cpu-baseline-tokens", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--profile-summary", action="store_true",
+                    help="write profiles/ summaries from rocprofv3 outputs (--trace-csv, --pmc-*, --cal-*)")
+    ap.add_argument("--trace-csv", help="kernel_trace.csv of a rocprofv3 --kernel-trace --stats run")
+    ap.add_argument("--pmc-fetch")
+    ap.add_argument("--pmc-write")
+    ap.add_argument("--cal-fetch")
+    ap.add_argument("--cal-write")
+    ap.add_argument("--pmc-calls", type=int, default=3, help="entry-point calls in the --pmc runs (warm-up + steps)")
+    ap.add_argument("--steps-profiled", type=int, default=10)
+    ap.add_argument("--profile-commands", help="the rocprofv3 command lines, one per line, recorded in the summaries")
     args = ap.parse_args()
+    if args.profile_summary:
+        sys.path.insert(0, str(ROOT))
+        return profile_summary(args)
     if args.copy_calibration:
         import torch
 
@@ -178,30 +367,34 @@ def main() -> int:
     kernels = {}
     for tag, ds in sorted(durations.items()):
         avg = statistics.fmean(ds)
-        kind, amount = work.get(tag, ("hbm", None))
         entry = {"avg_ms": round(avg, 4), "launches_per_step": len(ds) // args.steps}
-        if amount is not None:
-            rate = amount / (avg * 1e-3)
-            if kind == "mfma":
-                entry.update(tflops=round(rate / 1e12, 1), mfma_frac=round(rate / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
-            else:
-                entry.update(gbs=round(rate / 1e9, 1), hbm_frac=round(rate / 1e9 / HBM_PEAK_GBS, 4))
+        if tag in work:
+            flops, nbytes = work[tag]
+            entry["bound"] = bound_of(flops, nbytes)
+            if flops is not None:
+                tf = flops / (avg * 1e-3) / 1e12
+                entry.update(tflops=round(tf, 1), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
+            gbs = nbytes / (avg * 1e-3) / 1e9
+            entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
         kernels[tag] = entry
         log(f"  {tag:16s} {avg * 1e3:9.1f} us  {entry}")
     dominant = max(durations, key=lambda t: sum(durations[t]))
-    kind, amount = work[dominant]
+    flops, nbytes = work[dominant]
     avg_s = statistics.fmean(durations[dominant]) * 1e-3
-    if kind == "mfma":
-        achieved = amount / avg_s / 1e12
+    if bound_of(flops, nbytes) == "mfma":
+        achieved = flops / avg_s / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)}
     else:
-        achieved = amount / avg_s / 1e9
+        achieved = nbytes / avg_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4)}
-    roofline["kernel"] = dominant
-    roofline["work_per_launch"] = amount
     roofline["traffic"] = read_traffic(dominant, w.name)
+    roofline["kernel"] = dominant
+    roofline["algorithmic_bytes_per_launch"] = nbytes
+    roofline["flops_per_launch"] = flops
+    if flops is not None:
+        roofline["mfma_tflops"] = round(flops / avg_s / 1e12, 1)
     gemm_tags = [t for t in ("up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad") if t in durations]
     gemm_s = sum(statistics.fmean(durations[t]) for t in gemm_tags) * 1e-3
     gemm_tflops = w.gemm_flops() / gemm_s / 1e12 if gemm_s else None
