@@ -525,103 +525,158 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // ------------------------------------------------------ epilogue
   // Lane owns output row  wrow0 + i*32 + (lane & 31)  and columns
   // wcol0 + j*32 + 8*q + 4*(lane >> 5) + {0..3} holding acc[i][j][4q..4q+3].
-  const int col_lane = 4 * (lane >> 5);
+  if (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) {
+    // fp32 outputs (split-K partials, fp32 weight gradients): direct stores.
+    float* base = static_cast<float*>(p.C) + (EPI == EPI_F32 ? split * p.split_stride
+                                                                : static_cast<int64_t>(g) * p.stride_cg);
+    const int col_lane = 4 * (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < SM; ++i) {
-    const int row = wrow0 + i * 32 + (lane & 31);
-    if (row >= row_limit) continue;
-    if constexpr (EPI == EPI_SWIGLU_FWD) {
+    for (int i = 0; i < SM; ++i) {
+      const int row = wrow0 + i * 32 + l32;
+      if (row >= row_limit) continue;
 #pragma unroll
-      for (int j = 0; j < SN / 2; ++j) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = (n0 / 2) + wn * (WTN / 2) + j * 32 + 8 * q + col_lane;
-          if (col >= p.swiglu_I) continue;
-          float gt[4], up[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            gt[e] = acc[i][j][4 * q + e];
-            up[e] = acc[i][j + SN / 2][4 * q + e];
-          }
-          uint2 act;
-          act.x = pack_bf16x2(silu_f(gt[0]) * up[0], silu_f(gt[1]) * up[1]);
-          act.y = pack_bf16x2(silu_f(gt[2]) * up[2], silu_f(gt[3]) * up[3]);
-          *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = act;
-          if (p.C2) {
-            bf16_t* pre = static_cast<bf16_t*>(p.C2) + static_cast<int64_t>(row) * p.ldp;
-            uint2 gv, uv;
-            gv.x = pack_bf16x2(gt[0], gt[1]);
-            gv.y = pack_bf16x2(gt[2], gt[3]);
-            uv.x = pack_bf16x2(up[0], up[1]);
-            uv.y = pack_bf16x2(up[2], up[3]);
-            *reinterpret_cast<uint2*>(pre + col) = gv;
-            *reinterpret_cast<uint2*>(pre + p.swiglu_I + col) = uv;
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < SN; ++j) {
+      for (int j = 0; j < SN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = wcol0 + j * 32 + 8 * q + col_lane;
           if (col >= p.N) continue;
-          float v0 = acc[i][j][4 * q + 0], v1 = acc[i][j][4 * q + 1];
-          float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
-          if constexpr (EPI == EPI_BF16) {
-            uint2 o;
-            o.x = pack_bf16x2(v0, v1);
-            o.y = pack_bf16x2(v2, v3);
-            *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = o;
-          } else if constexpr (EPI == EPI_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(p.C) + split * p.split_stride +
-                                       static_cast<int64_t>(row) * p.ldc + col) = make_float4(v0, v1, v2, v3);
-          } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-            // v = d_act at (row, col..col+3); pre holds (gate | up).
-            const bf16_t* pre = p.P + static_cast<int64_t>(row) * p.ldp;
-            uint2 gw = *reinterpret_cast<const uint2*>(pre + col);
-            uint2 uw = *reinterpret_cast<const uint2*>(pre + p.N + col);
-            float gt[4] = {lo_bf16(gw.x), hi_bf16(gw.x), lo_bf16(gw.y), hi_bf16(gw.y)};
-            float up[4] = {lo_bf16(uw.x), hi_bf16(uw.x), lo_bf16(uw.y), hi_bf16(uw.y)};
-            float da[4] = {v0, v1, v2, v3};
-            float dg[4], du[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float s = 1.0f / (1.0f + __expf(-gt[e]));
-              float silu = gt[e] * s;
-              du[e] = da[e] * silu;
-              dg[e] = da[e] * up[e] * s * (1.0f + gt[e] * (1.0f - s));
-            }
-            bf16_t* out = static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc;
-            uint2 og, ou;
-            og.x = pack_bf16x2(dg[0], dg[1]);
-            og.y = pack_bf16x2(dg[2], dg[3]);
-            ou.x = pack_bf16x2(du[0], du[1]);
-            ou.y = pack_bf16x2(du[2], du[3]);
-            *reinterpret_cast<uint2*>(out + col) = og;
-            *reinterpret_cast<uint2*>(out + p.N + col) = ou;
-          } else {  // EPI_WGRAD: bf16 or f32 destination chosen by ldp (0 = bf16, 1 = f32)
-            int64_t off = static_cast<int64_t>(g) * p.stride_cg + static_cast<int64_t>(row) * p.ldc + col;
-            if (p.ldp) {
-              float4* dst = reinterpret_cast<float4*>(static_cast<float*>(p.C) + off);
-              if (p.accumulate) {
-                float4 o = *dst;
-                v0 += o.x; v1 += o.y; v2 += o.z; v3 += o.w;
-              }
-              *dst = make_float4(v0, v1, v2, v3);
-            } else {
-              uint2* dst = reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.C) + off);
-              if (p.accumulate) {
-                uint2 o = *dst;
-                v0 += lo_bf16(o.x); v1 += hi_bf16(o.x); v2 += lo_bf16(o.y); v3 += hi_bf16(o.y);
-              }
-              uint2 ob;
-              ob.x = pack_bf16x2(v0, v1);
-              ob.y = pack_bf16x2(v2, v3);
-              *dst = ob;
-            }
+          float4* dst = reinterpret_cast<float4*>(base + static_cast<int64_t>(row) * p.ldc + col);
+          float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          if (EPI == EPI_WGRAD && p.accumulate) {
+            const float4 o = *dst;
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
           }
+          *dst = v;
         }
+    }
+    return;
+  }
+
+  // bf16 outputs go through LDS so that every store is 16 bytes per lane and
+  // each wave store instruction writes whole 128-byte row segments.  Each wave
+  // rounds its [WTM][64] tile to bf16 into its own slice of the (now idle) ring
+  // and reads it back row-wise; no other wave touches the slice, so only the
+  // barrier that retires the ring is needed.  Staging layout (128-byte rows,
+  // 8 chunks of 16 bytes): chunk cc of row r sits at slot cc ^ stg_swizzle(r),
+  // and its two 8-byte halves are exchanged when bit 4 of r is set, which
+  // keeps the 8-byte writes, the row reads and the SwiGLU gate/up reads each on
+  // distinct banks.
+  static_assert(WTN == 64, "staged epilogue rows are 64 columns");
+  constexpr int REGION = WTM * WTN * 2;
+  constexpr int PER_STAGE = STAGE_BYTES / REGION;
+  static_assert(STAGE_BYTES % REGION == 0 && NWAVES <= PER_STAGE * STAGES, "ring too small to stage the tile");
+  barrier();  // every wave has finished reading the ring (its DMA retired above)
+  const int sidx = wave / PER_STAGE;
+  char* region = (sidx == 0 ? smem0 : sidx == 1 ? smem1 : sidx == 2 ? smem2 : sidx == 3 ? smem3 : smem4) +
+                 (wave - sidx * PER_STAGE) * REGION;
+  auto stg_swizzle = [](int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); };
+  {
+    const int lane_off = l32 * 128 + ((khalf ^ ((l32 >> 4) & 1)) << 3);
+    const int swz = stg_swizzle(l32);  // rows i*32 + l32 share bits 1-4 with l32
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+      for (int j = 0; j < SN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint2 v;
+          v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<uint2*>(region + i * 32 * 128 + lane_off + (((j * 4 + q) ^ swz) << 4)) = v;
+        }
+  }
+  auto swap_halves = [](uint4 v) { return make_uint4(v.z, v.w, v.x, v.y); };
+  auto to_f32x8 = [](uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = lo_bf16(w[e]);
+      f[2 * e + 1] = hi_bf16(w[e]);
+    }
+  };
+  auto to_bf16x8 = [](const float* f) {
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                      pack_bf16x2(f[6], f[7]));
+  };
+  auto round_bf16 = [](float x) { return bf16_to_f32(f32_to_bf16(x)); };
+
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    // Tile columns 0-31 are gate, 32-63 the matching up columns.  A lane takes
+    // one 8-column gate chunk and its up chunk: act = silu(gate) * up with the
+    // bf16 roundings of the reference (bf16 product output, silu output,
+    // product), and gate | up go to the saved pre-activation.
+    const int rr = lane >> 2, c4 = lane & 3;
+    const int act_col = (n0 / 2) + wn * (WTN / 2) + c4 * 8;
+    bf16_t* actp = static_cast<bf16_t*>(p.C);
+    bf16_t* prep = static_cast<bf16_t*>(p.C2);
+#pragma unroll
+    for (int n = 0; n < WTM / 16; ++n) {
+      const int r = 16 * n + rr;
+      const int swz = stg_swizzle(r);
+      uint4 gv = *reinterpret_cast<const uint4*>(region + r * 128 + ((c4 ^ swz) << 4));
+      uint4 uv = *reinterpret_cast<const uint4*>(region + r * 128 + (((c4 + 4) ^ swz) << 4));
+      if (n & 1) {
+        gv = swap_halves(gv);
+        uv = swap_halves(uv);
+      }
+      const int row = wrow0 + r;
+      if (row < row_limit && act_col < p.swiglu_I) {
+        float gf[8], uf[8], af[8];
+        to_f32x8(gv, gf);
+        to_f32x8(uv, uf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) af[e] = round_bf16(silu_f(gf[e])) * uf[e];
+        *reinterpret_cast<uint4*>(actp + static_cast<int64_t>(row) * p.ldc + act_col) = to_bf16x8(af);
+        if (prep) {
+          bf16_t* pr = prep + static_cast<int64_t>(row) * p.ldp;
+          *reinterpret_cast<uint4*>(pr + act_col) = gv;
+          *reinterpret_cast<uint4*>(pr + p.swiglu_I + act_col) = uv;
+        }
+      }
+    }
+  } else {
+    const int rr = lane >> 3, c8 = lane & 7;
+    const int col = wcol0 + c8 * 8;
+#pragma unroll
+    for (int n = 0; n < WTM / 8; ++n) {
+      const int r = 8 * n + rr;
+      uint4 v = *reinterpret_cast<const uint4*>(region + r * 128 + ((c8 ^ stg_swizzle(r)) << 4));
+      if ((n >> 1) & 1) v = swap_halves(v);
+      const int row = wrow0 + r;
+      if (row >= row_limit || col >= p.N) continue;
+      if constexpr (EPI == EPI_BF16) {
+        *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = v;
+      } else if constexpr (EPI == EPI_WGRAD) {
+        uint4* dst = reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(g) * p.stride_cg +
+                                              static_cast<int64_t>(row) * p.ldc + col);
+        if (p.accumulate) {
+          // Sum of the fp32 accumulator rounded to bf16 and the existing bf16
+          // gradient, rounded once more (torch's bf16 add of the two).
+          float a[8], o[8];
+          to_f32x8(v, a);
+          to_f32x8(*dst, o);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] += o[e];
+          v = to_bf16x8(a);
+        }
+        *dst = v;
+      } else {  // EPI_SWIGLU_BWD: v = d_act (bf16, as the reference's bf16 product); pre = (gate | up)
+        const bf16_t* pr = p.P + static_cast<int64_t>(row) * p.ldp;
+        float d[8], gf[8], uf[8], dg[8], du[8];
+        to_f32x8(v, d);
+        to_f32x8(*reinterpret_cast<const uint4*>(pr + col), gf);
+        to_f32x8(*reinterpret_cast<const uint4*>(pr + p.N + col), uf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // act = silu(gate) * up: d_up = d * silu(gate); d_silu = d * up;
+          // d_gate = d_silu * sigma (1 + gate (1 - sigma)).
+          const float sg = 1.0f / (1.0f + __expf(-gf[e]));
+          du[e] = d[e] * round_bf16(gf[e] * sg);
+          dg[e] = round_bf16(d[e] * uf[e]) * sg * (1.0f + gf[e] * (1.0f - sg));
+        }
+        bf16_t* out = static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc;
+        *reinterpret_cast<uint4*>(out + col) = to_bf16x8(dg);
+        *reinterpret_cast<uint4*>(out + p.N + col) = to_bf16x8(du);
       }
     }
   }
