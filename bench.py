@@ -97,41 +97,45 @@ _TAG_KERNELS = {
     "combine_fwd_kernel": "combine_fwd",
     "combine_bwd_kernel": "combine_bwd",
     "permute_bwd_kernel": "permute_bwd",
+    "swiglu_bwd_kernel": "down_dgrad",
 }
 _GEMM_RE = r"grouped_gemm_kernel<(\d), (true|false), (\d), moe::TileCfg<([0-9, ]+)>"
+# Expert-GEMM instantiations (mode, B K-contiguous, epilogue) -> the entry points
+# that launch them, in the order one step launches them.
+_GEMM_ORDER = {
+    (0, True, 2): ["up_fwd"],
+    (0, True, 0): ["down_fwd"],
+    (0, False, 0): ["down_dgrad", "up_dgrad"],  # backward runs the down projection first
+    (1, False, 4): ["down_wgrad", "up_wgrad"],
+}
 
 
-def tag_kernels(rows):
-    """Maps (kernel name, grid size) -> bench timer tag for the library's kernels.
+def tag_dispatches(names):
+    """Bench timer tag of each kernel dispatch, given kernel names in dispatch order.
 
     The expert GEMMs are the grouped_gemm instantiations sharing the tile
-    configuration of the SwiGLU forward (epilogue 2); the weight-gradient
-    instantiation serves both projections, told apart by grid size (the up
-    projection has twice the output tiles)."""
+    configuration of the SwiGLU forward (epilogue 2); an instantiation that
+    serves two entry points is told apart by its occurrence order (each step
+    launches them in a fixed order)."""
     import re
 
-    gemm = {}
-    for name, grid in rows:
-        m = re.search(_GEMM_RE, name)
+    parsed = [re.search(_GEMM_RE, n) for n in names]
+    expert_cfg = next((m[4] for m in parsed if m and m[3] == "2"), None)
+    seen = {}
+    tags = []
+    for n, m in zip(names, parsed):
         if m:
-            gemm[(name, grid)] = (int(m[1]), m[2] == "true", int(m[3]), m[4])
-    expert_cfg = next((v[3] for v in gemm.values() if v[2] == 2), None)
-    wgrad_grids = sorted({g for (n, g), v in gemm.items() if v[3] == expert_cfg and v[0] == 1})
-    out = {}
-    for name, grid in rows:
-        if (name, grid) in gemm:
-            mode, bkc, epi, cfg = gemm[(name, grid)]
-            if cfg == expert_cfg:
-                if mode == 1:
-                    out[(name, grid)] = "up_wgrad" if grid == wgrad_grids[-1] else "down_wgrad"
-                else:
-                    out[(name, grid)] = {(True, 2): "up_fwd", (True, 0): "down_fwd", (False, 3): "down_dgrad",
-                                         (False, 0): "up_dgrad"}.get((bkc, epi))
+            key = (int(m[1]), m[2] == "true", int(m[3]))
+            if m[4] == expert_cfg and key in _GEMM_ORDER:
+                order = _GEMM_ORDER[key]
+                i = seen.get(key, 0)
+                seen[key] = i + 1
+                tags.append(order[i % len(order)])
             else:
-                out[(name, grid)] = "router_fwd" if (mode, bkc) == (0, True) else "router_gemm_bwd"
+                tags.append("router_fwd" if key[:2] == (0, True) else "router_gemm_bwd")
             continue
-        out[(name, grid)] = next((t for k, t in _TAG_KERNELS.items() if f"moe::{k}" in name), None)
-    return out
+        tags.append(next((t for k, t in _TAG_KERNELS.items() if f"moe::{k}" in n or f" {k}(" in n or n.startswith(k)), None))
+    return tags
 
 
 def _read_csvs(d):
@@ -165,23 +169,20 @@ def profile_summary(args) -> int:
 
     # ---- kernel durations (per dispatch, from the --kernel-trace CSV of the --stats run)
     with open(args.trace_csv) as fh:
-        trace = list(csv.DictReader(fh))
+        trace = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
+    tags = tag_dispatches([r["Kernel_Name"] for r in trace])
     disp = defaultdict(list)
-    for r in trace:
-        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-        disp[(r["Kernel_Name"], grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    tags = tag_kernels(list(disp))
+    for r, tag in zip(trace, tags):
+        disp[(tag or "-", r["Kernel_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     grand = sum(sum(v) for v in disp.values())
     lines = [f"# rocprofv3 kernel statistics, workload {w.name} ({args.steps_profiled} timed + warm-up steps)",
              f"# command: {cmd.splitlines()[0] if cmd else '(not recorded)'}",
-             f"# {'tag':16s} {'calls':>6s} {'avg_us':>10s} {'total_us':>11s} {'pct':>6s}  kernel [grid threads]"]
+             f"# {'tag':16s} {'calls':>6s} {'avg_us':>10s} {'total_us':>11s} {'pct':>6s}  kernel"]
     per_tag = defaultdict(lambda: [0.0, 0])
-    for key, ds in sorted(disp.items(), key=lambda kv: -sum(kv[1])):
-        tag = tags.get(key) or "-"
+    for (tag, name), ds in sorted(disp.items(), key=lambda kv: -sum(kv[1])):
         total = sum(ds)
-        short = key[0].replace("moe::", "").split("(")[0][:100]
-        lines.append(f"  {tag:16s} {len(ds):6d} {total / len(ds):10.1f} {total:11.1f} {100 * total / grand:6.2f}  "
-                     f"{short} [{key[1]}]")
+        short = name.replace("moe::", "").split("(")[0][:100]
+        lines.append(f"  {tag:16s} {len(ds):6d} {total / len(ds):10.1f} {total:11.1f} {100 * total / grand:6.2f}  {short}")
         if tag != "-":
             per_tag[tag][0] += total
             per_tag[tag][1] = max(per_tag[tag][1], len(ds))
@@ -195,7 +196,7 @@ def profile_summary(args) -> int:
         acc = defaultdict(list)
         for r in _read_csvs(d):
             if r["Counter_Name"] == counter:
-                acc[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+                acc[(r["Kernel_Name"], int(r["Dispatch_Id"]))].append(float(r["Counter_Value"]))
         return acc
 
     def cal_factor(d, counter, expect_kib):
@@ -208,15 +209,14 @@ def profile_summary(args) -> int:
     w_fac, w_cal = cal_factor(args.cal_write, "WRITE_SIZE", 1 << 20)
     fetch = per_kernel(args.pmc_fetch, "FETCH_SIZE")
     write = per_kernel(args.pmc_write, "WRITE_SIZE")
-    ktags = tag_kernels(list(fetch))
     work = kernel_work(w, w.tokens, w.slots)
     by_tag = defaultdict(lambda: {"fetch": 0.0, "write": 0.0, "kernels": set()})
-    for key, vals in fetch.items():
-        tag = ktags.get(key)
-        if tag:
-            by_tag[tag]["fetch"] += sum(vals)
-            by_tag[tag]["write"] += sum(write.get(key, []))
-            by_tag[tag]["kernels"].add(key[0].replace("moe::", "").split("(")[0])
+    for runs, field in ((fetch, "fetch"), (write, "write")):
+        keys = sorted(runs, key=lambda k: k[1])  # dispatch order
+        for key, tag in zip(keys, tag_dispatches([k[0] for k in keys])):
+            if tag:
+                by_tag[tag][field] += sum(runs[key])
+                by_tag[tag]["kernels"].add(key[0].replace("moe::", "").split("(")[0])
     for tag, d in by_tag.items():
         calls = args.pmc_calls
         rd = d["fetch"] / calls * f_fac * 1024

@@ -16,7 +16,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmoe_mi355x.so"
+# MOE_MI355X_LIB selects another build of the same library (A/B comparisons).
+LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB") or Path(__file__).resolve().parent / "lib" / "libmoe_mi355x.so")
 ABI_VERSION = 1
 
 MOE_OK = 0

@@ -27,13 +27,14 @@
 // the launch index is remapped so that each XCD (blocks are dealt round-robin
 // over the 8 XCDs) gets a contiguous run of logical tiles and the sharing
 // happens in that XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm.h"
 
 namespace moe {
 
-enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU_FWD = 2, EPI_SWIGLU_BWD = 3, EPI_WGRAD = 4 };
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU_FWD = 2, EPI_WGRAD = 4 };
 enum { MODE_MG = 0, MODE_KG = 1 };
 
 constexpr int kNumXcd = 8;
@@ -43,7 +44,6 @@ struct GemmParams {
   const bf16_t* B;  // MG: per group (stride_bg) [N, K] or [K, N] (ldb);  KG: [rows, N] (ldb)
   void* C;          // MG: [rows, ldc];  KG: per group (stride_cg) [M, N] (ldc)
   void* C2;         // SWIGLU_FWD: pre-activation [rows, 2N] (may be null)
-  const bf16_t* P;  // SWIGLU_BWD: saved pre-activation [rows, 2N]
   const int32_t* offs;
   int G;
   int rows;     // total activation rows (M for MG; sum of K for KG)
@@ -52,9 +52,12 @@ struct GemmParams {
   int64_t stride_bg, stride_cg;
   uint32_t a_bytes;  // bytes addressable through the A buffer resource
   uint32_t b_bytes;  // bytes of one group's B (MG) or of all of B (KG)
+  uint32_t c_bytes;  // bytes of the output: all of C (MG), one group's (KG) or one split's (split-K)
+  uint32_t c2_bytes;  // SWIGLU_FWD: bytes of the pre-activation output (0 if none)
   int swiglu_I;      // SWIGLU_FWD: intermediate size I (weight rows gate: [0,I), up: [I,2I))
   int accumulate;
-  int n_tiles, m_tiles_max, total_blocks;
+  int n_tiles, m_tiles_max;
+  int total_tiles;     // exact tile count (grouped MG: worst case; the kernel counts the real ones)
   int k_splits, k_chunk;  // MG without groups: split the reduction, partial outputs stacked
   int64_t split_stride;   // elements between split partials of C
   int chunk_rows;         // KG without offs and G > 1: group g = rows [g*chunk_rows, ...)
@@ -71,42 +74,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
-
-// Find the group g whose tile range holds logical tile L, given per-group tile
-// counts ntile(g) = n_mult * ceil(cnt_g / BM).  Every wave of the block runs
-// this redundantly (no LDS, no barrier).  Returns false if L is past the end.
-template <int BM>
-__device__ __forceinline__ bool locate_group(const int32_t* offs, int G, int rows, int n_mult, int L, int& g_out,
-                                             int& tile0_out, int& row0_out, int& cnt_out) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int base = 0;  // tiles before this chunk
-  for (int c0 = 0; c0 < G; c0 += kWave) {
-    int g = c0 + lane;
-    int lo = 0, hi = 0;
-    if (g < G) {
-      // Clamped so that malformed offsets can never address rows outside [0, rows).
-      hi = min(max(offs[g], 0), rows);
-      lo = g ? min(max(offs[g - 1], 0), hi) : 0;
-    }
-    int cnt = hi - lo;
-    int nt = n_mult * ((cnt + BM - 1) / BM);
-    int incl = wave_inclusive_scan(nt);
-    unsigned long long hit = __ballot(g < G && L < base + incl);
-    if (hit) {
-      // Results are wave-uniform: move them to scalar registers so the
-      // compiler sees uniform control flow downstream.
-      int src = __ffsll(static_cast<long long>(hit)) - 1;
-      int excl = incl - nt;
-      g_out = __builtin_amdgcn_readfirstlane(c0 + src);
-      tile0_out = __builtin_amdgcn_readfirstlane(base + __builtin_amdgcn_readlane(excl, src));
-      row0_out = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(lo, src));
-      cnt_out = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(cnt, src));
-      return true;
-    }
-    base += __builtin_amdgcn_readlane(incl, kWave - 1);
-  }
-  return false;
-}
 
 // Total tiles over all groups, sum_g n_mult * ceil(cnt_g / BM) (wave-uniform).
 template <int BM>
@@ -132,8 +99,8 @@ struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int kThreads = 64 * WM * WN;
 };
-using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;    // expert GEMMs: 128 KiB LDS ring, 8 waves
-using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;  // router GEMMs (N = E = 128): 64 KiB ring
+using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;    // expert GEMMs: 128 KiB ring + 32 KiB staging, 8 waves
+using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;  // router GEMMs (N = E = 128): 64 KiB ring + 16 KiB staging
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
@@ -142,21 +109,71 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Calls f(std::integral_constant<int, i>{}) for i = 0 .. N-1 (compile-time unrolled).
-template <class F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char_t;
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
+// One 1 KiB LDS DMA: 64 lanes x 16 bytes from `rsrc` + voffset into LDS at
+// M0 (lane-ordered).  Issued from inline assembly so that the compiler does
+// not add its own (conservative) waits for the asynchronous LDS write: the
+// kernel waits for each k-tile with an explicit vmcnt and a barrier.
+// The descriptor is passed as four scalar words (base, base high, byte size,
+// format flags: the same words __builtin_amdgcn_make_buffer_rsrc builds).
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr)
+               : "memory");
+}
+
+__device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t w0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t w1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)) & 0xffffu;
+  const uint32_t w2 = __builtin_amdgcn_readfirstlane(bytes);
+  return u32x4_t{w0, w1, w2, 0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_address(const char* p) {
+  // The generic -> LDS address-space cast yields the 32-bit LDS byte address.
+  return (uint32_t)(uintptr_t)(const lds_char_t*)p;
+}
+
+// A wave-uniform pointer moved to scalar registers (buffer resources must be).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t off, uint4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{v.x, v.y, v.z, v.w}, rsrc, off, 0, 0);
+}
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ------------------------------------------------------------------ kernel
+//
+// Persistent blocks.  Block b runs on XCD b % 8 (launch indices are dealt
+// round-robin over the XCDs) and takes the tiles xidx, xidx + nbx, ... of its
+// XCD's contiguous share of the logical tiles, so the blocks of one XCD work
+// on neighbouring tiles (an expert's weight slab and its activation rows stay
+// in that XCD's L2).  With groups the real tile count is computed on the
+// device from `offs` (the grid is sized without a host sync).
+//
+// Each block runs one continuous stream of k-steps over all its tiles: a DMA
+// cursor fills the LDS ring STAGES-1 k-steps ahead of the compute cursor and
+// runs straight across tile boundaries, so the ring never drains between
+// tiles.  When the compute cursor finishes a tile, the wave writes it out
+// (epilogue) while the DMA of the next tile is already in flight; the tile
+// wait of the following STAGES-1 steps leaves that epilogue's stores
+// outstanding, so they drain in the background.  Every epilogue issues the
+// same number of store instructions per wave (out-of-range stores go to an
+// offset past the buffer resource and are dropped), which keeps those waits
+// exact.
 //
 // LDS layouts (per stage, per operand; 16-byte chunks, XOR-swizzled so that
 // the MFMA fragment reads are free of bank conflicts: gfx950 LDS serves
@@ -164,11 +181,11 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // lanes of a ds_read_b64_tr_b16 pass, must touch 64 distinct banks):
 //   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ kc_swizzle(r)
 //   M/N-contiguous operand [BK k][R cols]: chunk c of k-row kk at slot c ^ mc_swizzle(kk)
-// Each DMA instruction (buffer_load_dwordx4 ... lds) fills one contiguous
-// 1 KiB block lane by lane (lane l -> bytes 16l..16l+15), so a lane loads
-// whichever global chunk belongs at its slot.  K-contiguous fragments are one
-// ds_read_b128; M/N-contiguous fragments are two ds_read_b64_tr_b16, which
-// turn a 4 (k) x 16 (n) patch read by 16 lanes into 4 consecutive k per lane.
+// Each DMA instruction fills one contiguous 1 KiB block lane by lane (lane l
+// -> bytes 16l..16l+15), so a lane loads whichever global chunk belongs at
+// its slot.  K-contiguous fragments are one ds_read_b128; M/N-contiguous
+// fragments are two ds_read_b64_tr_b16, which turn a 4 (k) x 16 (n) patch read
+// by 16 lanes into 4 consecutive k per lane.
 
 // A ds_read_b128 pass reads one chunk of 16 consecutive rows: rows r and
 // r + 4k differ in bits 2-3, which move the chunk to another 16-byte bank group.
@@ -176,11 +193,23 @@ __device__ __forceinline__ constexpr int kc_swizzle(int r) { return (r >> 2) & 3
 // A transpose-read pass reads 32 columns (4 chunks) of 4 consecutive k-rows:
 // k-row kk & 3 selects the 64-byte bank quarter (needs >= 16 chunks per k-row).
 __device__ __forceinline__ constexpr int mc_swizzle(int kk) { return 4 * (kk & 3); }
+// Epilogue staging of a wave's 32 x 64 bf16 pass (128-byte rows): chunk cc of
+// row r at slot cc ^ stg_swizzle(r), its 8-byte halves exchanged when bit 4 of
+// r is set; the 8-byte writes, the row reads and the SwiGLU gate/up reads are
+// then each on distinct banks.
+__device__ __forceinline__ constexpr int stg_swizzle(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
+// Store instructions per wave per epilogue (all issued unconditionally).
+template <int EPI, int WTM, int SM, int SN>
+constexpr int epilogue_stores() {
+  return EPI == EPI_F32            ? SM * SN * 4
+         : EPI == EPI_SWIGLU_FWD  ? (WTM / 16) * 3
+                                  : WTM / 8;  // EPI_BF16; EPI_WGRAD (its fp32 variant issues more)
+}
 
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
 __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmParams p) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, STAGES = CFG::STAGES;
-  constexpr int kThreads = CFG::kThreads;
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM;  // wave tile rows
   constexpr int WTN = BN / WN;  // wave tile cols
@@ -192,235 +221,256 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
   constexpr int LPW = (NI_A + NI_B) / NWAVES;                  // ... per wave
+  constexpr int WAIT = (STAGES - 2) * LPW;                     // DMA younger than the k-tile waited for
+  constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
+  constexpr int SLOT = 32 * WTN * 2;                           // staging bytes per wave (one 32-row pass)
   static_assert(BK == 32, "swizzles and DMA mapping assume 32-deep k-tiles (4 chunks per K-contiguous row)");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 sub-tiles");
+  static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
   static_assert((NI_A + NI_B) % NWAVES == 0 && NI_A % LPW == 0, "DMA instructions split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
-  static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
+  static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+  static_assert(WAIT + NST < 64, "vmcnt range");
+  static_assert(A_KC || BM >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
+  static_assert(B_KC || BN >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
 
-  // One LDS array per ring stage: with distinct objects the compiler can tell
-  // the stage being read from the stages being filled by DMA.
-  __shared__ __attribute__((aligned(1024))) char smem0[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char smem1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char smem2[STAGES > 2 ? STAGE_BYTES : 16];
-  __shared__ __attribute__((aligned(1024))) char smem3[STAGES > 3 ? STAGE_BYTES : 16];
-  __shared__ __attribute__((aligned(1024))) char smem4[STAGES > 4 ? STAGE_BYTES : 16];
-  auto stage_ptr = [&](auto st) -> char* {
-    constexpr int S = decltype(st)::value;
-    if constexpr (S == 0) return smem0;
-    else if constexpr (S == 1) return smem1;
-    else if constexpr (S == 2) return smem2;
-    else if constexpr (S == 3) return smem3;
-    else return smem4;
-  };
+  __shared__ __attribute__((aligned(1024))) char ring[STAGES * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char staging[NWAVES * SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // Wave-uniform values live in scalar registers: buffer resources and the
-  // DMA LDS base (M0) must be uniform, or the compiler waterfalls each load.
+  // DMA LDS base (M0) must be uniform.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31;
+  const int khalf = lane >> 5;
 
-  // XCD-aware remap of the launch index to a logical tile index: blocks are
-  // dealt round-robin over the XCDs, so XCD x runs launch indices x, x + 8, ...;
-  // it gets the x-th contiguous share of the logical tiles.  With groups the
-  // grid is sized for the worst case, so the real tile count is computed here
-  // from `offs` and the shares are cut from it (otherwise the XCDs holding the
-  // upper end of the range would get no work).
-  const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd, xcd_idx = bid / kNumXcd;
-  int L;
-  if (MODE == MODE_MG && p.offs) {
-    const int real = count_tiles<BM>(p.offs, p.G, p.rows, p.n_tiles);
-    const int share = (real + kNumXcd - 1) / kNumXcd;
-    L = xcd * share + xcd_idx;
-    if (xcd_idx >= share || L >= real) return;
-  } else {
-    L = xcd * (p.total_blocks / kNumXcd) + xcd_idx;  // total_blocks is a multiple of kNumXcd
-  }
+  // ------------------------------------------------------ this block's tiles
+  const int nbx = gridDim.x / kNumXcd;  // the grid is a multiple of kNumXcd
+  const int xcd = blockIdx.x % kNumXcd, xidx = blockIdx.x / kNumXcd;
+  const int real = (MODE == MODE_MG && p.offs) ? count_tiles<BM>(p.offs, p.G, p.rows, p.n_tiles) : p.total_tiles;
+  const int share = (real + kNumXcd - 1) / kNumXcd;
+  const int first = xcd * share;
+  const int span = min(share, real - first);
+  const int ntiles = __builtin_amdgcn_readfirstlane(span > xidx ? (span - xidx + nbx - 1) / nbx : 0);
+  if (ntiles <= 0) return;
 
-  // ------------------------------------------------------ tile -> work
-  int g, m0, n0;               // group, first output row (within group for KG), first output col
-  int row_begin, row_end;      // MG: absolute activation rows of the group; KG: reduction rows
-  int split = 0, k_begin = 0;  // split-K partial index and its first reduction index
-  if constexpr (MODE == MODE_MG) {
-    if (p.offs) {
-      int tile0, row0, cnt;
-      if (!locate_group<BM>(p.offs, p.G, p.rows, p.n_tiles, L, g, tile0, row0, cnt)) return;
-      int local = L - tile0;
-      int mt_g = (cnt + BM - 1) / BM;
-      int nt = local / mt_g;
-      int mt = local - nt * mt_g;
-      row_begin = row0;
-      row_end = row0 + cnt;
-      m0 = row0 + mt * BM;  // absolute row
-      n0 = nt * BN;
+  // Lane l of a descriptor chunk describes block tile 64 * chunk + l:
+  // group, first output row (absolute for MG, within the group for KG),
+  // first output column, reduction rows [rb, re) (KG) or valid rows end (MG),
+  // split-K index.
+  struct Desc {
+    int g, m0, n0, rb, re, split;
+  };
+  auto describe = [&](int chunk) __attribute__((always_inline)) {
+    Desc d{0, 0, 0, 0, 0, 0};
+    const int j = chunk * kWave + lane;
+    const bool valid = j < ntiles;
+    const int L = first + xidx + j * nbx;
+    if constexpr (MODE == MODE_MG) {
+      if (p.offs) {
+        // Per-lane search of the group holding tile L over the cumulative
+        // per-group tile counts, one 64-group chunk at a time.
+        const int target = valid ? L : 0x7fffffff;
+        int found = 0, tg = 0, t0 = 0, r0 = 0, cn = 0, base = 0;
+        for (int c0 = 0; c0 < p.G; c0 += kWave) {
+          const int gg = c0 + lane;
+          int lo = 0, hi = 0;
+          if (gg < p.G) {
+            hi = min(max(p.offs[gg], 0), p.rows);  // clamped: malformed offsets never address outside [0, rows)
+            lo = gg ? min(max(p.offs[gg - 1], 0), hi) : 0;
+          }
+          const int cnt = hi - lo;
+          const int nt = p.n_tiles * ((cnt + BM - 1) / BM);
+          const int incl = wave_inclusive_scan(nt);
+          const int tot = __builtin_amdgcn_readlane(incl, kWave - 1);
+          const int t = target - base;
+          int q = 0;  // smallest q with incl[q] > t
+#pragma unroll
+          for (int s = kWave / 2; s >= 1; s >>= 1)
+            if (__shfl(incl, q + s - 1, kWave) <= t) q += s;
+          const int exq = __shfl(incl - nt, q, kWave), loq = __shfl(lo, q, kWave), cq = __shfl(cnt, q, kWave);
+          if (!found && t >= 0 && t < tot) {
+            found = 1;
+            tg = c0 + q;
+            t0 = base + exq;
+            r0 = loq;
+            cn = cq;
+          }
+          base += tot;
+        }
+        if (valid && found) {
+          const int local = L - t0;
+          const int mt_g = (cn + BM - 1) / BM;
+          const int nt = local / mt_g, mt = local - (local / mt_g) * mt_g;
+          d = Desc{tg, r0 + mt * BM, nt * BN, r0, r0 + cn, 0};
+        }
+      } else {
+        const int mtiles = (p.M + BM - 1) / BM;
+        const int per_split = mtiles * p.n_tiles;
+        const int split = L / per_split, local = L - split * per_split;
+        const int nt = local / mtiles, mt = local - nt * mtiles;
+        if (valid) d = Desc{0, mt * BM, nt * BN, 0, p.M, split};
+      }
     } else {
-      int mtiles = (p.M + BM - 1) / BM;
-      int per_split = mtiles * p.n_tiles;
-      split = L / per_split;
-      if (split >= p.k_splits) return;
-      int local = L - split * per_split;
-      g = 0;
-      int nt = local / mtiles;
-      int mt = local - nt * mtiles;
-      row_begin = 0;
-      row_end = p.M;
-      m0 = mt * BM;
-      n0 = nt * BN;
-      k_begin = split * p.k_chunk;
+      const int per_group = p.n_tiles * p.m_tiles_max;
+      const int g = L / per_group, local = L - g * per_group;
+      const int nt = local / p.m_tiles_max, mt = local - nt * p.m_tiles_max;
+      if (valid) {
+        int rb, re;
+        if (p.offs) {
+          re = min(max(p.offs[g], 0), p.rows);
+          rb = g ? min(max(p.offs[g - 1], 0), re) : 0;
+        } else {
+          rb = min(g * p.chunk_rows, p.rows);
+          re = min(rb + p.chunk_rows, p.rows);
+        }
+        d = Desc{g, mt * BM, nt * BN, rb, re, 0};
+      }
     }
-  } else {
-    const int per_group = p.n_tiles * p.m_tiles_max;
-    g = L / per_group;
-    if (g >= p.G) return;
-    int local = L - g * per_group;
-    int nt = local / p.m_tiles_max;
-    int mt = local - nt * p.m_tiles_max;
-    if (p.offs) {
-      row_end = min(max(p.offs[g], 0), p.rows);
-      row_begin = g ? min(max(p.offs[g - 1], 0), row_end) : 0;
-    } else {
-      row_begin = min(g * p.chunk_rows, p.rows);
-      row_end = min(row_begin + p.chunk_rows, p.rows);
-    }
-    m0 = mt * BM;
-    n0 = nt * BN;
-  }
-  g = __builtin_amdgcn_readfirstlane(g);
-  m0 = __builtin_amdgcn_readfirstlane(m0);
-  n0 = __builtin_amdgcn_readfirstlane(n0);
-  row_begin = __builtin_amdgcn_readfirstlane(row_begin);
-  row_end = __builtin_amdgcn_readfirstlane(row_end);
-  split = __builtin_amdgcn_readfirstlane(split);
-  k_begin = __builtin_amdgcn_readfirstlane(k_begin);
-  const bf16_t* Bg = (MODE == MODE_MG) ? p.B + static_cast<int64_t>(g) * p.stride_bg : p.B;
+    return d;
+  };
+  auto pick = [](int v, int j) { return __builtin_amdgcn_readlane(v, j & (kWave - 1)); };
 
-  // Reduction length for this tile.
-  const int Kred = (MODE == MODE_MG) ? min(p.K - k_begin, p.k_chunk) : (row_end - row_begin);
+  // Per-tile scalars shared by both cursors.
+  struct Tile {
+    int g, m0, n0, rb, re, split, k_begin, kred, nk;
+  };
+  auto tile_of = [&](const Desc& d, int j) __attribute__((always_inline)) {
+    Tile t;
+    t.g = pick(d.g, j);
+    t.m0 = pick(d.m0, j);
+    t.n0 = pick(d.n0, j);
+    t.rb = pick(d.rb, j);
+    t.re = pick(d.re, j);
+    t.split = pick(d.split, j);
+    t.k_begin = (MODE == MODE_MG) ? t.split * p.k_chunk : 0;
+    t.kred = (MODE == MODE_MG) ? min(p.K - t.k_begin, p.k_chunk) : (t.re - t.rb);
+    t.nk = t.kred > 0 ? (t.kred + BK - 1) / BK : 0;
+    return t;
+  };
 
-  if constexpr (MODE == MODE_KG) {
-    // Empty group: the weight gradient is zero (written below) or, when
-    // accumulating, unchanged.
-    if (Kred <= 0 && p.accumulate) return;
-  }
-
-  // Valid rows / columns of this wave's tile -> active 32x32 sub-tiles
-  // (wave-uniform; inactive sub-tiles skip their fragment reads and MFMAs).
-  // A SwiGLU tile keeps every sub-tile: gate and up halves pair up by index.
-  const int row_limit = (MODE == MODE_MG) ? row_end : p.M;
-  const int wrow0 = m0 + wm * WTM;
-  const int wcol0 = n0 + wn * WTN;
-  const int act_sm = __builtin_amdgcn_readfirstlane(min(SM, max(0, (row_limit - wrow0 + 31) / 32)));
-  const int act_sn =
-      __builtin_amdgcn_readfirstlane((EPI == EPI_SWIGLU_FWD) ? SN : min(SN, max(0, (p.N - wcol0 + 31) / 32)));
-  // Waves with no valid output rows or columns skip the MFMAs (they still
-  // take part in the DMA and the barriers).
-  const bool wave_active = act_sm > 0 && act_sn > 0;
-
-  f32x16_t acc[SM][SN];
-#pragma unroll
-  for (int i = 0; i < SM; ++i)
-#pragma unroll
-    for (int j = 0; j < SN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  // ------------------------------------------------------ DMA setup
+  // ------------------------------------------------------ DMA cursor
   // Wave w issues DMA instructions w*LPW .. w*LPW+LPW-1 of each k-tile; the
   // first NI_A belong to A, the rest to B (a wave's instructions never span
-  // both).  Per lane and instruction: the LDS byte offset within a stage, a
-  // fixed part of the global byte offset, and the k (K-contiguous: the k
-  // chunk; M/N-contiguous: the k row) it adds per k-tile.
+  // both).  Per lane and instruction: the LDS byte offset within a stage
+  // (wave-uniform), the k (K-contiguous: the chunk's k; M/N-contiguous: the
+  // k-row) it adds per k-tile, and a per-tile base offset (kOOB if the row or
+  // column is outside the tile's valid range).
   const bool dma_a = (wave * LPW) < NI_A;  // wave-uniform
-  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
-  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bg, p.b_bytes);
-  uint32_t dma_lds[LPW];   // stage-relative LDS byte offset of this wave's instruction j
-  uint32_t dma_base[LPW];  // K-contiguous: row byte offset + chunk bytes (kOOB if the row is invalid);
-                           // M/N-contiguous: column byte offset (kOOB if the column is invalid)
-  int dma_k[LPW];          // K-contiguous: k of the chunk; M/N-contiguous: k row within the tile
+  const bool dma_kc = dma_a ? A_KC : B_KC;
+  const u32x4_t rsA = rsrc_words(p.A, p.a_bytes);
+  const uint32_t mc_ld = static_cast<uint32_t>(dma_a ? p.lda : p.ldb) * 2u;
+  int dma_lds[LPW], dma_k[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int inst = wave * LPW + j;
     const bool is_a = inst < NI_A;
-    const int li = is_a ? inst : inst - NI_A;  // instruction index within the operand
-    dma_lds[j] = (is_a ? 0 : A_BYTES) + li * 1024;
-    const bool kc = is_a ? A_KC : B_KC;
-    if (kc) {
-      // 16 rows x 4 chunks: lane -> row li*16 + lane/4, slot lane%4.
+    const int li = is_a ? inst : inst - NI_A;
+    dma_lds[j] = __builtin_amdgcn_readfirstlane((is_a ? 0 : A_BYTES) + li * 1024);
+    if (is_a ? A_KC : B_KC) {
       const int r = li * 16 + (lane >> 2);
-      const int c = (lane & 3) ^ kc_swizzle(r);
-      dma_k[j] = c * 8;
-      bool ok;
-      uint32_t row_bytes;
-      if (is_a) {
-        const int grow = m0 + r;
-        ok = grow < row_end;
-        row_bytes = static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u;
-      } else {
-        int wrow;
-        if constexpr (EPI == EPI_SWIGLU_FWD) {
-          // Tile row r -> (wave column, sub-tile, half): the first SN/2
-          // sub-tiles of each wave column are gate rows, the rest the
-          // matching up rows.
-          const int wcol = r / WTN;
-          const int within = r % WTN;
-          const int sn = within / 32;
-          const int half = sn / (SN / 2);
-          const int act_col = (n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
-          ok = act_col < p.swiglu_I;
-          wrow = half * p.swiglu_I + act_col;
-        } else {
-          wrow = n0 + r;
-          ok = wrow < p.N;
-        }
-        row_bytes = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u;
-      }
-      dma_base[j] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u : kOOB;
+      dma_k[j] = ((lane & 3) ^ kc_swizzle(r)) * 8;
     } else {
-      // k-rows of R columns: R/8 chunks per k-row, 64/(R/8) k-rows per instruction.
-      const int R = is_a ? BM : BN;
-      const int cpk = R / 8;
-      const int kk = li * (64 / cpk) + lane / cpk;
-      const int c = (lane % cpk) ^ mc_swizzle(kk);
-      const int col = (is_a ? m0 : n0) + c * 8;
-      const bool ok = col < (is_a ? p.M : p.N);
-      dma_k[j] = kk;
-      dma_base[j] = ok ? static_cast<uint32_t>(col) * 2u : kOOB;
+      const int cpk = (is_a ? BM : BN) / 8;
+      dma_k[j] = li * (64 / cpk) + lane / cpk;
     }
   }
-  const int mc_row0 = (MODE == MODE_KG) ? row_begin : k_begin;  // global row of tile k = 0 (M/N-contiguous)
-  const uint32_t mc_ld = static_cast<uint32_t>(dma_a ? p.lda : p.ldb) * 2u;
 
-  // Issue the DMA of k-tile kt into ring stage ST.  The operand a wave loads
-  // is wave-uniform: its buffer resource and offset formula are selected
-  // without branches, so every wave runs the same straight-line code.
-  auto issue_tile = [&](int kt, auto st) {
-    const int k0 = kt * BK;
-    char* stage = stage_ptr(st);
-    const __amdgpu_buffer_rsrc_t rs = dma_a ? rsA : rsB;
-    const bool kc = dma_a ? A_KC : B_KC;
+  Desc dd = describe(0);
+  int dchunk = 0;
+  int dj = 0, dk = 0;  // DMA cursor: block tile and k-step
+  Tile dt;
+  u32x4_t rsB = rsrc_words(p.B, p.b_bytes);
+  uint32_t dma_base[LPW];
+  int d_mc_row0 = 0;
+  // Sets the DMA cursor on block tile j (skipping tiles without k-steps);
+  // past the last tile the cursor issues out-of-range loads (zeros).
+  auto dma_seek = [&](int j) __attribute__((always_inline)) {
+    for (;; ++j) {
+      if (j >= ntiles) {
+        dj = ntiles;
+        return;
+      }
+      if ((j >> 6) != dchunk) {
+        dchunk = j >> 6;
+        dd = describe(dchunk);
+      }
+      dt = tile_of(dd, j);
+      if (dt.nk > 0) break;
+    }
+    dj = j;
+    dk = 0;
+    if (MODE == MODE_MG) rsB = rsrc_words(p.B + static_cast<int64_t>(dt.g) * p.stride_bg, p.b_bytes);
+    d_mc_row0 = (MODE == MODE_KG) ? dt.rb : dt.k_begin;
+#pragma unroll
+    for (int j2 = 0; j2 < LPW; ++j2) {
+      const int inst = wave * LPW + j2;
+      const bool is_a = inst < NI_A;
+      const int li = is_a ? inst : inst - NI_A;
+      if (is_a ? A_KC : B_KC) {
+        const int r = li * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ kc_swizzle(r);
+        bool ok;
+        uint32_t row_bytes;
+        if (is_a) {
+          const int grow = dt.m0 + r;
+          ok = grow < dt.re;
+          row_bytes = static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u;
+        } else {
+          int wrow;
+          if constexpr (EPI == EPI_SWIGLU_FWD) {
+            // Tile row r -> (wave column, sub-tile, half): the first SN/2
+            // sub-tiles of each wave column are gate rows, the rest the
+            // matching up rows.
+            const int wcol = r / WTN;
+            const int within = r % WTN;
+            const int sn = within / 32;
+            const int half = sn / (SN / 2);
+            const int act_col = (dt.n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
+            ok = act_col < p.swiglu_I;
+            wrow = half * p.swiglu_I + act_col;
+          } else {
+            wrow = dt.n0 + r;
+            ok = wrow < p.N;
+          }
+          row_bytes = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u;
+        }
+        dma_base[j2] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u : kOOB;
+      } else {
+        const int cpk = (is_a ? BM : BN) / 8;
+        const int kk = li * (64 / cpk) + lane / cpk;
+        const int c = (lane % cpk) ^ mc_swizzle(kk);
+        const int col = (is_a ? dt.m0 : dt.n0) + c * 8;
+        dma_base[j2] = col < (is_a ? p.M : p.N) ? static_cast<uint32_t>(col) * 2u : kOOB;
+      }
+    }
+  };
+  // Issues the DMA of the cursor's next k-step into ring stage `st`.  Every
+  // call issues exactly LPW instructions per wave.
+  auto dma_issue = [&](int st) __attribute__((always_inline)) {
+    const bool live = dj < ntiles;
+    const int k0 = dk * BK;
+    u32x4_t rs;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rs[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(dma_a ? rsA[w] : rsB[w]));
+    const uint32_t stage_lds = lds_address(ring) + st * STAGE_BYTES;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int kk = k0 + dma_k[j];  // K-contiguous: k of the chunk; M/N-contiguous: k row
-      const uint32_t kc_off = dma_base[j] + static_cast<uint32_t>(k_begin + k0) * 2u;
-      const uint32_t mc_off = static_cast<uint32_t>(mc_row0 + kk) * mc_ld + dma_base[j];
-      const uint32_t off = (kk < Kred && dma_base[j] != kOOB) ? (kc ? kc_off : mc_off) : kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(stage + dma_lds[j]), 16, off, 0, 0, 0);
+      const int kk = k0 + dma_k[j];
+      const uint32_t kc_off = dma_base[j] + static_cast<uint32_t>(dt.k_begin + k0) * 2u;
+      const uint32_t mc_off = static_cast<uint32_t>(d_mc_row0 + kk) * mc_ld + dma_base[j];
+      const uint32_t off = (live && kk < dt.kred && dma_base[j] != kOOB) ? (dma_kc ? kc_off : mc_off) : kOOB;
+      dma16(rs, off, __builtin_amdgcn_readfirstlane(stage_lds + dma_lds[j]));
     }
+    if (live && ++dk == dt.nk) dma_seek(dj + 1);
   };
 
   // ------------------------------------------------------ fragment reads
-  // Each lane's byte offset within a stage is precomputed per fragment
-  // class, so every fragment address is the stage array plus one lane
-  // offset plus a constant.  Short address chains keep the per-stage alias
-  // scopes that the compiler attaches to LDS accesses (it follows only a few
-  // levels of address arithmetic); without them a fragment read waits for
-  // every DMA in flight.
-  const int l32 = lane & 31;
-  const int khalf = lane >> 5;
-  // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk 2 ks + khalf.
-  // Fragment rows start on 32-row boundaries, so row & 15 == l32 & 15.
+  // Each lane's byte offset within a stage is precomputed per fragment class;
+  // a fragment address is the stage base plus a lane offset plus a constant.
+  // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk
+  // 2 ks + khalf; fragment rows start on 32-row boundaries (row & 15 == l32 & 15).
   int a_kc[2], b_kc[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -432,8 +482,6 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // k-rows 16 ks + 8 (q/2) + 4 h + i/4 and columns tile_col + 16 (q%2) + 4 (i%4).
   // The swizzle depends only on k-row & 3 == i/4, so each 32-column sub-tile
   // has one lane offset; ks and h add constants.
-  static_assert(A_KC || BM >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
-  static_assert(B_KC || BN >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
   const int q16 = lane >> 4, i16 = lane & 15;
   const int tr_krow = 8 * (q16 >> 1) + (i16 >> 2);
   const int tr_col = 16 * (q16 & 1) + 4 * (i16 & 3);
@@ -446,30 +494,42 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   for (int t = 0; t < SN; ++t)
     b_mc[t] = A_BYTES + tr_krow * BN * 2 + ((((wn * WTN + 32 * t + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
 
-  auto ld_frag_kc = [&](const char* stage, int lane_off, int row0_const) -> bf16x8_t {
-    return *reinterpret_cast<const bf16x8_t*>(stage + lane_off + row0_const * 64);
-  };
-  // Sub-tile t (32 columns) of a wave tile with R columns per k-row.
-  auto ld_frag_mc = [&](const char* stage, const int* lane_off, int R, int t, int ks) -> bf16x8_t {
-    const char* p = stage + lane_off[t] + 16 * ks * R * 2;
-    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
-    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * R * 2));
-    typedef short i16x8_t __attribute__((ext_vector_type(8)));
-    i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8_t, v);
+  f32x16_t acc[SM][SN];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+      for (int j = 0; j < SN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   };
 
-  auto compute_tile = [&](auto st) {
-    const char* stage = stage_ptr(st);
+  auto compute_stage = [&](const char* stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[SM], bfr[SN];
 #pragma unroll
-      for (int i = 0; i < SM; ++i)
-        af[i] = A_KC ? ld_frag_kc(stage, a_kc[ks], i * 32) : ld_frag_mc(stage, a_mc, BM, i, ks);
+      for (int i = 0; i < SM; ++i) {
+        if constexpr (A_KC) {
+          af[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * 32 * 64);
+        } else {
+          const char* q = stage + a_mc[i] + 16 * ks * BM * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(q + 4 * BM * 2));
+          af[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
 #pragma unroll
-      for (int j = 0; j < SN; ++j)
-        bfr[j] = B_KC ? ld_frag_kc(stage, b_kc[ks], j * 32) : ld_frag_mc(stage, b_mc, BN, j, ks);
+      for (int j = 0; j < SN; ++j) {
+        if constexpr (B_KC) {
+          bfr[j] = *reinterpret_cast<const bf16x8_t*>(stage + b_kc[ks] + j * 32 * 64);
+        } else {
+          const char* q = stage + b_mc[j] + 16 * ks * BN * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(q + 4 * BN * 2));
+          bfr[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
 #pragma unroll
       for (int i = 0; i < SM; ++i)
 #pragma unroll
@@ -480,111 +540,19 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     }
   };
 
-  // Workgroup barrier without a memory fence: a fenced barrier would make the
-  // compiler drain every outstanding DMA (vmcnt(0)) each k-tile.  The empty
-  // asm statements keep LDS accesses from moving across it; the DMA of the
-  // tile about to be read is waited for explicitly with vmcnt.
+  // Workgroup barrier without a memory fence (a fenced barrier would drain
+  // every outstanding DMA); the empty asm statements keep LDS accesses from
+  // moving across it.
   auto barrier = [] {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
-  // STAGES-deep ring: k-tile kt lives in stage kt % STAGES; the DMA of tile
-  // kt + STAGES - 1 is issued right after the barrier that retires tile
-  // kt - 1.  Every step issues exactly LPW DMA instructions per wave (past
-  // the last tile they are all out of range and only write zeros to a stage
-  // that is never read), so the wait for tile kt is always the same vmcnt.
-  //
-  // The steady-state loop runs whole groups of STAGES steps with no per-step
-  // guard, so every stage index is a compile-time constant and the
-  // compiler's LDS-DMA wait tracking (one alias scope per stage array) stays
-  // exact across the back edge: a fragment read waits only for the DMA of
-  // its own stage, which the explicit vmcnt above already retired.  Guarded
-  // steps inside the loop would merge paths with different DMA histories at
-  // the back edge and make the compiler drain every DMA (vmcnt(0)) before
-  // each step's reads.  The last nk % STAGES steps run after the loop.
-  const int nk = (Kred + BK - 1) / BK;
-  auto step = [&](int kt, auto st) {
-    constexpr int S = decltype(st)::value;
-    wait_vmcnt<(STAGES - 2) * LPW>();
-    barrier();
-    issue_tile(kt + STAGES - 1, std::integral_constant<int, (S + STAGES - 1) % STAGES>{});
-    if (wave_active) compute_tile(st);
-  };
-  if (nk > 0) {
-    static_for<STAGES - 1>([&](auto i) { issue_tile(i, i); });
-    int kt = 0;
-    for (; kt + STAGES <= nk; kt += STAGES) static_for<STAGES>([&](auto i) { step(kt + i, i); });
-    static_for<STAGES - 1>([&](auto i) {
-      if (kt + i < nk) step(kt + i, i);
-    });
-    wait_vmcnt<0>();  // retire the trailing out-of-range DMA before the LDS is released
-  }
-
   // ------------------------------------------------------ epilogue
-  // Lane owns output row  wrow0 + i*32 + (lane & 31)  and columns
-  // wcol0 + j*32 + 8*q + 4*(lane >> 5) + {0..3} holding acc[i][j][4q..4q+3].
-  if (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) {
-    // fp32 outputs (split-K partials, fp32 weight gradients): direct stores.
-    float* base = static_cast<float*>(p.C) + (EPI == EPI_F32 ? split * p.split_stride
-                                                                : static_cast<int64_t>(g) * p.stride_cg);
-    const int col_lane = 4 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < SM; ++i) {
-      const int row = wrow0 + i * 32 + l32;
-      if (row >= row_limit) continue;
-#pragma unroll
-      for (int j = 0; j < SN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = wcol0 + j * 32 + 8 * q + col_lane;
-          if (col >= p.N) continue;
-          float4* dst = reinterpret_cast<float4*>(base + static_cast<int64_t>(row) * p.ldc + col);
-          float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          if (EPI == EPI_WGRAD && p.accumulate) {
-            const float4 o = *dst;
-            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
-          }
-          *dst = v;
-        }
-    }
-    return;
-  }
-
-  // bf16 outputs go through LDS so that every store is 16 bytes per lane and
-  // each wave store instruction writes whole 128-byte row segments.  Each wave
-  // rounds its [WTM][64] tile to bf16 into its own slice of the (now idle) ring
-  // and reads it back row-wise; no other wave touches the slice, so only the
-  // barrier that retires the ring is needed.  Staging layout (128-byte rows,
-  // 8 chunks of 16 bytes): chunk cc of row r sits at slot cc ^ stg_swizzle(r),
-  // and its two 8-byte halves are exchanged when bit 4 of r is set, which
-  // keeps the 8-byte writes, the row reads and the SwiGLU gate/up reads each on
-  // distinct banks.
-  static_assert(WTN == 64, "staged epilogue rows are 64 columns");
-  constexpr int REGION = WTM * WTN * 2;
-  constexpr int PER_STAGE = STAGE_BYTES / REGION;
-  static_assert(STAGE_BYTES % REGION == 0 && NWAVES <= PER_STAGE * STAGES, "ring too small to stage the tile");
-  barrier();  // every wave has finished reading the ring (its DMA retired above)
-  const int sidx = wave / PER_STAGE;
-  char* region = (sidx == 0 ? smem0 : sidx == 1 ? smem1 : sidx == 2 ? smem2 : sidx == 3 ? smem3 : smem4) +
-                 (wave - sidx * PER_STAGE) * REGION;
-  auto stg_swizzle = [](int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); };
-  {
-    const int lane_off = l32 * 128 + ((khalf ^ ((l32 >> 4) & 1)) << 3);
-    const int swz = stg_swizzle(l32);  // rows i*32 + l32 share bits 1-4 with l32
-#pragma unroll
-    for (int i = 0; i < SM; ++i)
-#pragma unroll
-      for (int j = 0; j < SN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint2 v;
-          v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
-          v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          *reinterpret_cast<uint2*>(region + i * 32 * 128 + lane_off + (((j * 4 + q) ^ swz) << 4)) = v;
-        }
-  }
+  // Lane owns output row  wrow0 + i*32 + l32  and columns
+  // wcol0 + j*32 + 8*q + 4*khalf + {0..3} holding acc[i][j][4q..4q+3].
+  char* slot = staging + wave * SLOT;  // this wave's staging slot (no other wave touches it)
   auto swap_halves = [](uint4 v) { return make_uint4(v.z, v.w, v.x, v.y); };
   auto to_f32x8 = [](uint4 v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -599,87 +567,209 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
                       pack_bf16x2(f[6], f[7]));
   };
   auto round_bf16 = [](float x) { return bf16_to_f32(f32_to_bf16(x)); };
+  const __amdgpu_buffer_rsrc_t rsC2 = make_rsrc(p.C2, p.c2_bytes);  // SwiGLU pre-activation (0 bytes if absent)
 
-  if constexpr (EPI == EPI_SWIGLU_FWD) {
-    // Tile columns 0-31 are gate, 32-63 the matching up columns.  A lane takes
-    // one 8-column gate chunk and its up chunk: act = silu(gate) * up with the
-    // bf16 roundings of the reference (bf16 product output, silu output,
-    // product), and gate | up go to the saved pre-activation.
-    const int rr = lane >> 2, c4 = lane & 3;
-    const int act_col = (n0 / 2) + wn * (WTN / 2) + c4 * 8;
-    bf16_t* actp = static_cast<bf16_t*>(p.C);
-    bf16_t* prep = static_cast<bf16_t*>(p.C2);
+  auto epilogue = [&](const Tile& t) __attribute__((always_inline)) {
+    const int wrow0 = t.m0 + wm * WTM;
+    const int wcol0 = t.n0 + wn * WTN;
+    const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
+    // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
+    const int esize = (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) ? 4 : 2;
+    const int64_t c_base = (MODE == MODE_KG) ? static_cast<int64_t>(t.g) * p.stride_cg
+                         : (EPI == EPI_F32)  ? static_cast<int64_t>(t.split) * p.split_stride
+                                             : 0;
+    const __amdgpu_buffer_rsrc_t rsC = make_rsrc(uniform_ptr(static_cast<char*>(p.C) + c_base * esize), p.c_bytes);
+    if (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) {
+      // fp32 outputs (split-K partials, fp32 weight gradients): direct 16-byte stores.
 #pragma unroll
-    for (int n = 0; n < WTM / 16; ++n) {
-      const int r = 16 * n + rr;
-      const int swz = stg_swizzle(r);
-      uint4 gv = *reinterpret_cast<const uint4*>(region + r * 128 + ((c4 ^ swz) << 4));
-      uint4 uv = *reinterpret_cast<const uint4*>(region + r * 128 + (((c4 + 4) ^ swz) << 4));
-      if (n & 1) {
-        gv = swap_halves(gv);
-        uv = swap_halves(uv);
+      for (int i = 0; i < SM; ++i) {
+        const int row = wrow0 + i * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int col = wcol0 + j * 32 + 8 * q + 4 * khalf;
+            const uint32_t off = (row < row_limit && col < p.N)
+                                     ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldc) +
+                                        static_cast<uint32_t>(col)) * 4u
+                                     : kOOB;
+            float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+            if (EPI == EPI_WGRAD && p.accumulate) {
+              const uint4 o = load16(rsC, off);
+              v.x += __uint_as_float(o.x);
+              v.y += __uint_as_float(o.y);
+              v.z += __uint_as_float(o.z);
+              v.w += __uint_as_float(o.w);
+            }
+            store16(rsC, off, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                         __float_as_uint(v.w)));
+          }
       }
-      const int row = wrow0 + r;
-      if (row < row_limit && act_col < p.swiglu_I) {
-        float gf[8], uf[8], af[8];
-        to_f32x8(gv, gf);
-        to_f32x8(uv, uf);
+      return;
+    }
+    // bf16 outputs go through this wave's LDS slot one 32-row pass at a time,
+    // so that every store is 16 bytes per lane over whole 128-byte row segments.
+    const int stg_lane = l32 * 128 + ((khalf ^ ((l32 >> 4) & 1)) << 3);
+    const int stg_swz = stg_swizzle(l32);
+    const int rr8 = lane >> 3, c8 = lane & 7;  // row-read lane mapping: row 8n + rr8, chunk c8
 #pragma unroll
-        for (int e = 0; e < 8; ++e) af[e] = round_bf16(silu_f(gf[e])) * uf[e];
-        *reinterpret_cast<uint4*>(actp + static_cast<int64_t>(row) * p.ldc + act_col) = to_bf16x8(af);
-        if (prep) {
-          bf16_t* pr = prep + static_cast<int64_t>(row) * p.ldp;
-          *reinterpret_cast<uint4*>(pr + act_col) = gv;
-          *reinterpret_cast<uint4*>(pr + p.swiglu_I + act_col) = uv;
+    for (int i = 0; i < SM; ++i) {
+      const int prow0 = wrow0 + i * 32;  // first output row of this pass
+      // Output offsets of this pass's row reads and, when accumulating, the
+      // existing gradient, loaded before the staging so that their latency
+      // overlaps it.
+      uint32_t out_off[4];
+      uint4 in0[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int row = prow0 + 8 * n + rr8, col = wcol0 + c8 * 8;
+        const bool ok = row < row_limit && col < p.N;
+        out_off[n] = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldc) + static_cast<uint32_t>(col)) * 2u
+                        : kOOB;
+        if constexpr (EPI == EPI_WGRAD) {
+          if (p.accumulate) in0[n] = load16(rsC, out_off[n]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint2 v;
+          v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<uint2*>(slot + stg_lane + (((j * 4 + q) ^ stg_swz) << 4)) = v;
+        }
+      if constexpr (EPI == EPI_SWIGLU_FWD) {
+        // Slot columns 0-31 are gate, 32-63 the matching up columns.  A lane
+        // takes one 8-column gate chunk and its up chunk: act = silu(gate) * up
+        // with the reference's bf16 roundings (bf16 GEMM output, silu output,
+        // product); gate | up go to the saved pre-activation.
+        const int rr = lane >> 2, c4 = lane & 3;
+        const int act_col = (t.n0 / 2) + wn * (WTN / 2) + c4 * 8;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          const int r = 16 * n + rr;
+          const int swz = stg_swizzle(r);
+          uint4 gv = *reinterpret_cast<const uint4*>(slot + r * 128 + ((c4 ^ swz) << 4));
+          uint4 uv = *reinterpret_cast<const uint4*>(slot + r * 128 + (((c4 + 4) ^ swz) << 4));
+          if (n & 1) {
+            gv = swap_halves(gv);
+            uv = swap_halves(uv);
+          }
+          const int row = prow0 + r;
+          const bool ok = row < row_limit && act_col < p.swiglu_I;
+          float gf[8], uf[8], af[8];
+          to_f32x8(gv, gf);
+          to_f32x8(uv, uf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) af[e] = round_bf16(silu_f(gf[e])) * uf[e];
+          const uint32_t act_off = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldc) +
+                                         static_cast<uint32_t>(act_col)) * 2u
+                                      : kOOB;
+          const uint32_t pre_off = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldp) +
+                                         static_cast<uint32_t>(act_col)) * 2u
+                                      : kOOB;
+          store16(rsC, act_off, to_bf16x8(af));
+          store16(rsC2, pre_off, gv);
+          store16(rsC2, ok ? pre_off + static_cast<uint32_t>(p.swiglu_I) * 2u : kOOB, uv);
+        }
+      } else {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const int r = 8 * n + rr8;
+          uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((c8 ^ stg_swizzle(r)) << 4));
+          if ((n >> 1) & 1) v = swap_halves(v);
+          if constexpr (EPI == EPI_BF16) {
+            store16(rsC, out_off[n], v);
+          } else if constexpr (EPI == EPI_WGRAD) {
+            if (p.accumulate) {
+              // The fp32 accumulator rounded to bf16 plus the existing bf16
+              // gradient, rounded once more (torch's bf16 add of the two).
+              float a[8], o[8];
+              to_f32x8(v, a);
+              to_f32x8(in0[n], o);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) a[e] += o[e];
+              v = to_bf16x8(a);
+            }
+            store16(rsC, out_off[n], v);
+          }
         }
       }
     }
-  } else {
-    const int rr = lane >> 3, c8 = lane & 7;
-    const int col = wcol0 + c8 * 8;
-#pragma unroll
-    for (int n = 0; n < WTM / 8; ++n) {
-      const int r = 8 * n + rr;
-      uint4 v = *reinterpret_cast<const uint4*>(region + r * 128 + ((c8 ^ stg_swizzle(r)) << 4));
-      if ((n >> 1) & 1) v = swap_halves(v);
-      const int row = wrow0 + r;
-      if (row >= row_limit || col >= p.N) continue;
-      if constexpr (EPI == EPI_BF16) {
-        *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = v;
-      } else if constexpr (EPI == EPI_WGRAD) {
-        uint4* dst = reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(g) * p.stride_cg +
-                                              static_cast<int64_t>(row) * p.ldc + col);
-        if (p.accumulate) {
-          // Sum of the fp32 accumulator rounded to bf16 and the existing bf16
-          // gradient, rounded once more (torch's bf16 add of the two).
-          float a[8], o[8];
-          to_f32x8(v, a);
-          to_f32x8(*dst, o);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] += o[e];
-          v = to_bf16x8(a);
+  };
+
+  // ------------------------------------------------------ compute cursor
+  Desc cd = dd;
+  int cchunk = 0;
+  int cj = 0, ck = 0;
+  Tile ct;
+  bool c_active = false;
+  // Sets the compute cursor on block tile j.  Tiles without k-steps (empty
+  // groups of a weight gradient) are written out here directly: zeros, or
+  // nothing when accumulating.  Returns false past the last tile.
+  int relax = 0;  // steps whose tile wait still leaves the last epilogue's stores in flight
+  auto compute_seek = [&](int j) -> bool __attribute__((always_inline)) {
+    for (;; ++j) {
+      if (j >= ntiles) return false;
+      if ((j >> 6) != cchunk) {
+        cchunk = j >> 6;
+        cd = describe(cchunk);
+      }
+      ct = tile_of(cd, j);
+      zero_acc();
+      if (ct.nk > 0) break;
+      if constexpr (MODE == MODE_KG) {  // (MG tiles always have k-steps)
+        if (!p.accumulate) {
+          epilogue(ct);
+          relax = STAGES - 1;
         }
-        *dst = v;
-      } else {  // EPI_SWIGLU_BWD: v = d_act (bf16, as the reference's bf16 product); pre = (gate | up)
-        const bf16_t* pr = p.P + static_cast<int64_t>(row) * p.ldp;
-        float d[8], gf[8], uf[8], dg[8], du[8];
-        to_f32x8(v, d);
-        to_f32x8(*reinterpret_cast<const uint4*>(pr + col), gf);
-        to_f32x8(*reinterpret_cast<const uint4*>(pr + p.N + col), uf);
+      }
+    }
+    cj = j;
+    ck = 0;
+    const int row_limit = (MODE == MODE_MG) ? ct.re : p.M;
+    const int wrow0 = ct.m0 + wm * WTM, wcol0 = ct.n0 + wn * WTN;
+    // Waves whose rows or columns all lie outside the tile skip the MFMAs
+    // (they still take part in the DMA and the barriers).
+    c_active = wrow0 < row_limit && (EPI == EPI_SWIGLU_FWD || wcol0 < p.N);
+    return true;
+  };
+
+  // ------------------------------------------------------ the k-step stream
+  dma_seek(0);
+  const bool any = compute_seek(0);
+  // Stores of tiles written out above precede every DMA, so the plain tile
+  // wait already covers them.
+  relax = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // act = silu(gate) * up: d_up = d * silu(gate); d_silu = d * up;
-          // d_gate = d_silu * sigma (1 + gate (1 - sigma)).
-          const float sg = 1.0f / (1.0f + __expf(-gf[e]));
-          du[e] = d[e] * round_bf16(gf[e] * sg);
-          dg[e] = round_bf16(d[e] * uf[e]) * sg * (1.0f + gf[e] * (1.0f - sg));
-        }
-        bf16_t* out = static_cast<bf16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc;
-        *reinterpret_cast<uint4*>(out + col) = to_bf16x8(dg);
-        *reinterpret_cast<uint4*>(out + p.N + col) = to_bf16x8(du);
+  for (int s = 0; s < STAGES - 1; ++s) dma_issue(s);
+  int cstage = 0, dstage = STAGES - 1;
+  if (any) {
+    for (;;) {
+      // k-tile of this step landed: this wave's DMA (all but the WAIT younger
+      // instructions, plus the last epilogue's stores while they drain), then
+      // every wave's, via the barrier; the barrier also retires the reads of
+      // the stage the next DMA overwrites.
+      if (relax > 0) {
+        wait_vmcnt<WAIT + NST>();
+        --relax;
+      } else {
+        wait_vmcnt<WAIT>();
+      }
+      barrier();
+      dma_issue(dstage);
+      dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
+      if (c_active) compute_stage(ring + cstage * STAGE_BYTES);
+      cstage = cstage + 1 == STAGES ? 0 : cstage + 1;
+      if (++ck == ct.nk) {
+        epilogue(ct);
+        relax = STAGES - 1;
+        if (!compute_seek(cj + 1)) break;
       }
     }
   }
+  wait_vmcnt<0>();  // retire the trailing DMA (zeros) before the LDS is released
 }
 
 // ------------------------------------------------------------ host side
@@ -690,13 +780,27 @@ int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 constexpr int64_t kMaxRsrcBytes = (1ll << 31) - 64;
 
-int set_bytes(GemmParams& p, int64_t a_bytes, int64_t b_bytes, const char* name) {
-  MOE_REQUIRE(a_bytes < kMaxRsrcBytes && b_bytes < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED,
-              "%s: operand of %lld / %lld bytes exceeds the 2 GiB buffer-resource range", name, (long long)a_bytes,
-              (long long)b_bytes);
+int set_bytes(GemmParams& p, int64_t a_bytes, int64_t b_bytes, int64_t c_bytes, const char* name) {
+  MOE_REQUIRE(a_bytes < kMaxRsrcBytes && b_bytes < kMaxRsrcBytes && c_bytes < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED,
+              "%s: operand of %lld / %lld / %lld bytes exceeds the 2 GiB buffer-resource range", name,
+              (long long)a_bytes, (long long)b_bytes, (long long)c_bytes);
   p.a_bytes = static_cast<uint32_t>(a_bytes);
   p.b_bytes = static_cast<uint32_t>(b_bytes);
+  p.c_bytes = static_cast<uint32_t>(c_bytes);
   return MOE_OK;
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
@@ -708,19 +812,33 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
   // Output column tiles; a SwiGLU tile covers BN/2 act columns (gate + up rows).
   p.n_tiles = (EPI == EPI_SWIGLU_FWD) ? (p.swiglu_I + CFG::BN / 2 - 1) / (CFG::BN / 2)
                                       : (p.N + CFG::BN - 1) / CFG::BN;
-  int64_t blocks;
+  int64_t tiles;  // exact, or (grouped MG) the worst case; the kernel counts the real tiles itself
   if (MODE == MODE_MG) {
     p.m_tiles_max = (p.M + CFG::BM - 1) / CFG::BM + (p.offs ? p.G : 0);
-    blocks = static_cast<int64_t>(p.m_tiles_max) * p.n_tiles * (p.offs ? 1 : p.k_splits);
+    tiles = static_cast<int64_t>(p.m_tiles_max) * p.n_tiles * (p.offs ? 1 : p.k_splits);
   } else {
     p.m_tiles_max = (p.M + CFG::BM - 1) / CFG::BM;
-    blocks = static_cast<int64_t>(p.G) * p.m_tiles_max * p.n_tiles;
+    tiles = static_cast<int64_t>(p.G) * p.m_tiles_max * p.n_tiles;
   }
-  if (blocks <= 0) return MOE_OK;
-  MOE_REQUIRE(blocks < (1ll << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", name);
-  p.total_blocks = round_up(static_cast<int>(blocks), kNumXcd);
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>), dim3(p.total_blocks), dim3(CFG::kThreads), 0,
-                     stream, p);
+  if (tiles <= 0) return MOE_OK;
+  MOE_REQUIRE(tiles < (1ll << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", name);
+  p.total_tiles = static_cast<int>(tiles);
+  // Persistent grid: as many blocks as fit at once (capped by the tile
+  // count), a multiple of the XCD count.
+  static int occ = 0;
+  if (!occ) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>,
+                                                     CFG::kThreads, 0) != hipSuccess || n <= 0)
+      n = 1;
+    occ = n;
+  }
+  const int64_t resident = static_cast<int64_t>(device_cus()) * occ / kNumXcd * kNumXcd;
+  const int grid = static_cast<int>(std::max<int64_t>(kNumXcd, std::min<int64_t>(round_up(static_cast<int>(tiles),
+                                                                                          kNumXcd),
+                                                                                 resident)));
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>), dim3(grid), dim3(CFG::kThreads), 0, stream,
+                     p);
   return launch_status(name);
 }
 
@@ -757,7 +875,8 @@ int router_logits_partials(const bf16_t* x, const bf16_t* wr, float* partials, i
   p.k_splits = splits;
   p.k_chunk = k_chunk;
   p.split_stride = static_cast<int64_t>(T) * E;
-  int rc = set_bytes(p, static_cast<int64_t>(T) * H * 2, static_cast<int64_t>(E) * H * 2, "router logits");
+  int rc = set_bytes(p, static_cast<int64_t>(T) * H * 2, static_cast<int64_t>(E) * H * 2,
+                     static_cast<int64_t>(T) * E * 4, "router logits");
   if (rc) return rc;
   return launch<MODE_MG, true, EPI_F32, SmallTile>(p, stream, "router logits (split-K)");
 }
@@ -781,7 +900,8 @@ int router_wgrad_partials(const bf16_t* dl, const bf16_t* x, float* partials, in
   p.ldc = H;
   p.ldp = 1;  // f32 destination
   p.stride_cg = static_cast<int64_t>(E) * H;
-  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(T) * H * 2, "router wgrad");
+  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(T) * H * 2,
+                     static_cast<int64_t>(E) * H * 4, "router wgrad");
   if (rc) return rc;
   return launch<MODE_KG, false, EPI_WGRAD, SmallTile>(p, stream, "router wgrad (row chunks)");
 }
@@ -799,9 +919,48 @@ int router_dgrad(const bf16_t* dl, const bf16_t* wr, bf16_t* dx, int T, int H, i
   p.lda = E;
   p.ldb = H;
   p.ldc = H;
-  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(E) * H * 2, "router dgrad");
+  int rc = set_bytes(p, static_cast<int64_t>(T) * E * 2, static_cast<int64_t>(E) * H * 2,
+                     static_cast<int64_t>(T) * H * 2, "router dgrad");
   if (rc) return rc;
   return launch<MODE_MG, false, EPI_BF16, SmallTile>(p, stream, "router dgrad");
+}
+
+// SwiGLU backward, elementwise and in place over d_pre [rows, 2I]: the up
+// half holds d_act (the bf16 input-gradient GEMM output) on entry; on exit
+// d_pre = (d_gate | d_up) with the reference's bf16 roundings:
+//   d_up = d * silu(gate),  d_silu = d * up,  d_gate = d_silu * s (1 + gate (1 - s)).
+// One lane per 8 columns (16-byte loads and stores).
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(bf16_t* __restrict__ d_pre, const bf16_t* __restrict__ pre,
+                                                         unsigned rows, unsigned I) {
+  const unsigned cpr = I / 8;  // 8-column chunks per half row
+  const unsigned total = rows * cpr;
+  for (unsigned c = blockIdx.x * blockDim.x + threadIdx.x; c < total; c += gridDim.x * blockDim.x) {
+    const unsigned r = c / cpr, k = (c - r * cpr) * 8;
+    bf16_t* dr = d_pre + static_cast<size_t>(r) * 2 * I;
+    const bf16_t* pr = pre + static_cast<size_t>(r) * 2 * I;
+    const uint4 dv = *reinterpret_cast<const uint4*>(dr + I + k);
+    const uint4 gv = *reinterpret_cast<const uint4*>(pr + k);
+    const uint4 uv = *reinterpret_cast<const uint4*>(pr + I + k);
+    const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t og[4], ou[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float dg2[2], du2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float d = h ? hi_bf16(dw[e]) : lo_bf16(dw[e]);
+        const float g = h ? hi_bf16(gw[e]) : lo_bf16(gw[e]);
+        const float u = h ? hi_bf16(uw[e]) : lo_bf16(uw[e]);
+        const float sg = 1.0f / (1.0f + __expf(-g));
+        du2[h] = d * bf16_to_f32(f32_to_bf16(g * sg));
+        dg2[h] = bf16_to_f32(f32_to_bf16(d * u)) * sg * (1.0f + g * (1.0f - sg));
+      }
+      og[e] = pack_bf16x2(dg2[0], dg2[1]);
+      ou[e] = pack_bf16x2(du2[0], du2[1]);
+    }
+    *reinterpret_cast<uint4*>(dr + k) = make_uint4(og[0], og[1], og[2], og[3]);
+    *reinterpret_cast<uint4*>(dr + I + k) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  }
 }
 
 }  // namespace moe
@@ -830,7 +989,9 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
   p.ldp = 2 * I;
   p.stride_bg = 2 * I * H;
   p.swiglu_I = static_cast<int>(I);
-  if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
+  if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, M * I * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
+  p.c2_bytes = pre ? static_cast<uint32_t>(M * 2 * I * 2) : 0u;  // < a_bytes-range: checked below
+  MOE_REQUIRE(M * 2 * I * 2 < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED, "swiglu fwd: pre-activation exceeds 2 GiB");
   return launch<MODE_MG, true, EPI_SWIGLU_FWD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
 }
 
@@ -853,7 +1014,7 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
   p.ldb = K;
   p.ldc = N;
   p.stride_bg = N * K;
-  if ((rc = set_bytes(p, M * K * 2, N * K * 2, "moe_grouped_gemm_fwd"))) return rc;
+  if ((rc = set_bytes(p, M * K * 2, N * K * 2, M * N * 2, "moe_grouped_gemm_fwd"))) return rc;
   return launch<MODE_MG, true, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_fwd");
 }
 
@@ -889,24 +1050,25 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   p.ldb = K;
   p.ldc = K;
   p.stride_bg = N * K;
-  if ((rc = set_bytes(p, M * N * 2, N * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
+  if ((rc = set_bytes(p, M * N * 2, N * K * 2, M * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
   return launch<MODE_MG, false, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
 }
 
 extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down, const void* pre,
                                                  const int32_t* offs, int64_t G, int64_t M, int64_t H, int64_t I,
                                                  void* d_pre, void* stream) {
-  // d_act[M,I] = dy[M,H] . w_down[g] (w_down [G,H,I]); fused SwiGLU backward.
+  // d_act[M,I] = dy[M,H] . w_down[g] (w_down [G,H,I]) into the up half of
+  // d_pre, then the SwiGLU backward in place.
   int rc = check_common(dy, w_down, offs, G, M, I, H);
   if (rc) return rc;
   MOE_REQUIRE(pre && d_pre && aligned16(pre) && aligned16(d_pre), MOE_ERR_INVALID,
               "dgrad swiglu: bad pre/d_pre pointer");
+  MOE_REQUIRE(M * I / 8 < (1ll << 31), MOE_ERR_UNSUPPORTED, "dgrad swiglu: too many rows");
   if (M == 0) return MOE_OK;
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(dy);
   p.B = static_cast<const bf16_t*>(w_down);
-  p.C = d_pre;
-  p.P = static_cast<const bf16_t*>(pre);
+  p.C = static_cast<bf16_t*>(d_pre) + I;
   p.offs = offs;
   p.G = static_cast<int>(G);
   p.rows = p.M = static_cast<int>(M);
@@ -915,10 +1077,15 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   p.lda = H;
   p.ldb = I;
   p.ldc = 2 * I;
-  p.ldp = 2 * I;
   p.stride_bg = H * I;
-  if ((rc = set_bytes(p, M * H * 2, H * I * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
-  return launch<MODE_MG, false, EPI_SWIGLU_BWD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad_swiglu_bwd");
+  if ((rc = set_bytes(p, M * H * 2, H * I * 2, (M * 2 * I - I) * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
+  hipStream_t st = as_stream(stream);
+  if ((rc = launch<MODE_MG, false, EPI_BF16, BigTile>(p, st, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
+  const int64_t chunks = M * I / 8;
+  const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 4096));
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(grid), dim3(256), 0, st, static_cast<bf16_t*>(d_pre),
+                     static_cast<const bf16_t*>(pre), static_cast<unsigned>(M), static_cast<unsigned>(I));
+  return launch_status("moe_grouped_gemm_dgrad_swiglu_bwd (swiglu)");
 }
 
 extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
@@ -944,6 +1111,6 @@ extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32
   p.stride_cg = N * K;
   p.accumulate = accumulate ? 1 : 0;
   p.chunk_rows = static_cast<int>(M);
-  if ((rc = set_bytes(p, M * N * 2, M * K * 2, "moe_grouped_gemm_wgrad"))) return rc;
+  if ((rc = set_bytes(p, M * N * 2, M * K * 2, N * K * (dw_is_f32 ? 4 : 2), "moe_grouped_gemm_wgrad"))) return rc;
   return launch<MODE_KG, false, EPI_WGRAD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
 }
