@@ -99,8 +99,15 @@ struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int kThreads = 64 * WM * WN;
 };
-using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;    // expert GEMMs: 128 KiB ring + 32 KiB staging, 8 waves
-using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;  // router GEMMs (N = E = 128): 64 KiB ring + 16 KiB staging
+// Expert GEMMs over grouped rows (MG): 512-row tiles, so that an expert of up
+// to 512 rows is one m-tile and its weights stream through LDS once per
+// n-tile; 120 KiB ring + 32 KiB staging, 8 waves.
+using TallTile = TileCfg<512, 128, 32, 4, 2, 3>;
+// Expert weight gradients (KG): 128 KiB ring + 32 KiB staging, 8 waves.
+using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;
+// Router GEMMs (N = E = 128): 64 KiB ring + 16 KiB staging, 4 waves.
+using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;
+using ExpertTile = TallTile;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
@@ -120,8 +127,12 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // kernel waits for each k-tile with an explicit vmcnt and a barrier.
 // The descriptor is passed as four scalar words (base, base high, byte size,
 // format flags: the same words __builtin_amdgcn_make_buffer_rsrc builds).
+// The compiler's hazard recognizer does not look inside the asm, so the asm
+// supplies the wait states itself: 5 cover a VALU write of the descriptor
+// SGPRs (v_readfirstlane, or a v_readlane restoring spilled SGPRs) right
+// before the load, and the 1 needed after the write of M0.
 __device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr)
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr)
                : "memory");
 }
 
@@ -220,13 +231,14 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
-  constexpr int LPW = (NI_A + NI_B) / NWAVES;                  // ... per wave
+  constexpr int LPW_A = NI_A / NWAVES, LPW_B = NI_B / NWAVES;  // ... per wave and operand
+  constexpr int LPW = LPW_A + LPW_B;
   constexpr int WAIT = (STAGES - 2) * LPW;                     // DMA younger than the k-tile waited for
   constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
   constexpr int SLOT = 32 * WTN * 2;                           // staging bytes per wave (one 32-row pass)
   static_assert(BK == 32, "swizzles and DMA mapping assume 32-deep k-tiles (4 chunks per K-contiguous row)");
   static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
-  static_assert((NI_A + NI_B) % NWAVES == 0 && NI_A % LPW == 0, "DMA instructions split evenly over waves");
+  static_assert(NI_A % NWAVES == 0 && NI_B % NWAVES == 0, "DMA instructions of each operand split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
   static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
   static_assert(WAIT + NST < 64, "vmcnt range");
@@ -351,29 +363,33 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   };
 
   // ------------------------------------------------------ DMA cursor
-  // Wave w issues DMA instructions w*LPW .. w*LPW+LPW-1 of each k-tile; the
-  // first NI_A belong to A, the rest to B (a wave's instructions never span
-  // both).  Per lane and instruction: the LDS byte offset within a stage
-  // (wave-uniform), the k (K-contiguous: the chunk's k; M/N-contiguous: the
-  // k-row) it adds per k-tile, and a per-tile base offset (kOOB if the row or
-  // column is outside the tile's valid range).
-  const bool dma_a = (wave * LPW) < NI_A;  // wave-uniform
-  const bool dma_kc = dma_a ? A_KC : B_KC;
+  // Each k-tile is NI_A + NI_B DMA instructions of 1 KiB; wave w issues A
+  // instructions w*LPW_A .. w*LPW_A+LPW_A-1 (its slots j < LPW_A) and B
+  // instructions w*LPW_B .. w*LPW_B+LPW_B-1 (slots j >= LPW_A).  Per lane and
+  // slot: the LDS byte offset within a stage (wave-uniform), the k
+  // (K-contiguous: the chunk's k; M/N-contiguous: the k-row) it adds per
+  // k-tile, and a per-tile base offset (kOOB if the row or column is outside
+  // the tile's valid range).
   const u32x4_t rsA = rsrc_words(p.A, p.a_bytes);
-  const uint32_t mc_ld = static_cast<uint32_t>(dma_a ? p.lda : p.ldb) * 2u;
-  int dma_lds[LPW], dma_k[LPW];
+  // Slot j's instruction: operand and index within the operand's k-tile.
+  auto slot_inst = [&](int j, bool& is_a) {
+    is_a = j < LPW_A;
+    return is_a ? wave * LPW_A + j : wave * LPW_B + (j - LPW_A);
+  };
+  int dma_lds[LPW], dma_k[LPW], dma_col[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
-    const int inst = wave * LPW + j;
-    const bool is_a = inst < NI_A;
-    const int li = is_a ? inst : inst - NI_A;
+    bool is_a;
+    const int li = slot_inst(j, is_a);
     dma_lds[j] = __builtin_amdgcn_readfirstlane((is_a ? 0 : A_BYTES) + li * 1024);
+    dma_col[j] = 0;
     if (is_a ? A_KC : B_KC) {
       const int r = li * 16 + (lane >> 2);
       dma_k[j] = ((lane & 3) ^ kc_swizzle(r)) * 8;
     } else {
-      const int cpk = (is_a ? BM : BN) / 8;
+      const int cpk = (is_a ? BM : BN) / 8;  // 16-byte chunks per k-row
       dma_k[j] = li * (64 / cpk) + lane / cpk;
+      dma_col[j] = ((lane % cpk) ^ mc_swizzle(dma_k[j])) * 8;  // first of the chunk's 8 columns
     }
   }
 
@@ -382,14 +398,18 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   int dj = 0, dk = 0;  // DMA cursor: block tile and k-step
   Tile dt;
   u32x4_t rsB = rsrc_words(p.B, p.b_bytes);
-  uint32_t dma_base[LPW];
-  int d_mc_row0 = 0;
+  // Per slot: the lane's byte offset at the tile's first k-step (kOOB if the
+  // row or column lies outside the tile, or past the last tile); a k-step
+  // adds a uniform amount to it.
+  uint32_t dma_pre[LPW];
   // Sets the DMA cursor on block tile j (skipping tiles without k-steps);
   // past the last tile the cursor issues out-of-range loads (zeros).
   auto dma_seek = [&](int j) __attribute__((always_inline)) {
     for (;; ++j) {
       if (j >= ntiles) {
         dj = ntiles;
+#pragma unroll
+        for (int j2 = 0; j2 < LPW; ++j2) dma_pre[j2] = kOOB;
         return;
       }
       if ((j >> 6) != dchunk) {
@@ -402,12 +422,11 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     dj = j;
     dk = 0;
     if (MODE == MODE_MG) rsB = rsrc_words(p.B + static_cast<int64_t>(dt.g) * p.stride_bg, p.b_bytes);
-    d_mc_row0 = (MODE == MODE_KG) ? dt.rb : dt.k_begin;
+    const int mc_row0 = (MODE == MODE_KG) ? dt.rb : dt.k_begin;
 #pragma unroll
     for (int j2 = 0; j2 < LPW; ++j2) {
-      const int inst = wave * LPW + j2;
-      const bool is_a = inst < NI_A;
-      const int li = is_a ? inst : inst - NI_A;
+      bool is_a;
+      const int li = slot_inst(j2, is_a);
       if (is_a ? A_KC : B_KC) {
         const int r = li * 16 + (lane >> 2);
         const int c = (lane & 3) ^ kc_swizzle(r);
@@ -436,46 +455,71 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
           }
           row_bytes = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u;
         }
-        dma_base[j2] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u : kOOB;
+        dma_pre[j2] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u + static_cast<uint32_t>(dt.k_begin) * 2u : kOOB;
       } else {
-        const int cpk = (is_a ? BM : BN) / 8;
-        const int kk = li * (64 / cpk) + lane / cpk;
-        const int c = (lane % cpk) ^ mc_swizzle(kk);
-        const int col = (is_a ? dt.m0 : dt.n0) + c * 8;
-        dma_base[j2] = col < (is_a ? p.M : p.N) ? static_cast<uint32_t>(col) * 2u : kOOB;
+        const int col = (is_a ? dt.m0 : dt.n0) + dma_col[j2];
+        const uint32_t ld = static_cast<uint32_t>(is_a ? p.lda : p.ldb) * 2u;
+        dma_pre[j2] = col < (is_a ? p.M : p.N)
+                          ? static_cast<uint32_t>(mc_row0 + dma_k[j2]) * ld + static_cast<uint32_t>(col) * 2u
+                          : kOOB;
       }
     }
   };
-  // Issues the DMA of the cursor's next k-step into ring stage `st`.  Every
-  // call issues exactly LPW instructions per wave.
-  auto dma_issue = [&](int st) __attribute__((always_inline)) {
-    const bool live = dj < ntiles;
+  // The DMA of the cursor's next k-step into ring stage `st`, in three parts:
+  // dma_prepare computes the per-lane offsets of the wave's LPW slots,
+  // dma_fire(j) issues slot j, dma_advance moves the cursor.  The compute
+  // loop fires the slots between its MFMA groups, so that the texture unit
+  // works through the k-step's DMA while the matrix cores run instead of
+  // taking every wave's burst at once.  Every k-step fires exactly LPW
+  // instructions per wave.
+  uint32_t doff[LPW], dlds[LPW];
+  u32x4_t ra, rb;
+  auto dma_prepare = [&](int st) __attribute__((always_inline)) {
     const int k0 = dk * BK;
-    u32x4_t rs;
+    const int k_left = dt.kred - k0;  // k (K-contiguous) or k-rows (M/N-contiguous) left in the tile
 #pragma unroll
-    for (int w = 0; w < 4; ++w) rs[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(dma_a ? rsA[w] : rsB[w]));
+    for (int w = 0; w < 4; ++w) {
+      ra[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsA[w]));
+      rb[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsB[w]));
+    }
     const uint32_t stage_lds = lds_address(ring) + st * STAGE_BYTES;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int kk = k0 + dma_k[j];
-      const uint32_t kc_off = dma_base[j] + static_cast<uint32_t>(dt.k_begin + k0) * 2u;
-      const uint32_t mc_off = static_cast<uint32_t>(d_mc_row0 + kk) * mc_ld + dma_base[j];
-      const uint32_t off = (live && kk < dt.kred && dma_base[j] != kOOB) ? (dma_kc ? kc_off : mc_off) : kOOB;
-      dma16(rs, off, __builtin_amdgcn_readfirstlane(stage_lds + dma_lds[j]));
+      const bool is_a = j < LPW_A;
+      const uint32_t step = (is_a ? A_KC : B_KC) ? 2u : static_cast<uint32_t>(is_a ? p.lda : p.ldb) * 2u;
+      // Past the last tile dma_pre is kOOB and stays out of range (the
+      // added offset is below the 2 GiB operand limit).
+      doff[j] = dma_k[j] < k_left ? dma_pre[j] + static_cast<uint32_t>(k0) * step : kOOB;
+      dlds[j] = __builtin_amdgcn_readfirstlane(stage_lds + dma_lds[j]);
     }
-    if (live && ++dk == dt.nk) dma_seek(dj + 1);
+  };
+  auto dma_fire = [&](int j) __attribute__((always_inline)) { dma16(j < LPW_A ? ra : rb, doff[j], dlds[j]); };
+  auto dma_advance = [&]() __attribute__((always_inline)) {
+    if (dj < ntiles && ++dk == dt.nk) dma_seek(dj + 1);
+  };
+  auto dma_issue = [&](int st) __attribute__((always_inline)) {
+    dma_prepare(st);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) dma_fire(j);
+    dma_advance();
   };
 
   // ------------------------------------------------------ fragment reads
+  // A wave's SM row sub-tiles are interleaved with the other wave rows':
+  // sub-tile i covers tile rows sub_row(i) .. +31, so that the sub-tiles of a
+  // partly filled tile spread over all waves (and SIMDs).  Its SN column
+  // sub-tiles are contiguous: columns wn*WTN + 32 j.
+  //
   // Each lane's byte offset within a stage is precomputed per fragment class;
   // a fragment address is the stage base plus a lane offset plus a constant.
   // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk
   // 2 ks + khalf; fragment rows start on 32-row boundaries (row & 15 == l32 & 15).
+  auto sub_row = [&](int i) { return (wm + WM * i) * 32; };
   int a_kc[2], b_kc[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int lane_off = l32 * 64 + (((2 * ks + khalf) ^ kc_swizzle(l32)) << 4);
-    a_kc[ks] = wm * WTM * 64 + lane_off;
+    a_kc[ks] = sub_row(0) * 64 + lane_off;
     b_kc[ks] = A_BYTES + wn * WTN * 64 + lane_off;
   }
   // M/N-contiguous [BK k-rows][R cols] (transpose reads): lane = 16 q + i reads
@@ -489,7 +533,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   int a_mc[SM], b_mc[SN];
 #pragma unroll
   for (int t = 0; t < SM; ++t)
-    a_mc[t] = tr_krow * BM * 2 + ((((wm * WTM + 32 * t + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
+    a_mc[t] = tr_krow * BM * 2 + ((((sub_row(t) + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
 #pragma unroll
   for (int t = 0; t < SN; ++t)
     b_mc[t] = A_BYTES + tr_krow * BN * 2 + ((((wn * WTN + 32 * t + tr_col) >> 3) ^ mc_swizzle(tr_krow)) << 4) + half8;
@@ -504,14 +548,18 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   };
 
-  auto compute_stage = [&](const char* stage) __attribute__((always_inline)) {
+  // One k-tile of MFMAs over the first `na` row sub-tiles (the others hold no
+  // rows of this tile; `na` is wave-uniform, so the guards are scalar
+  // branches), with the prepared DMA slots fired between the MFMA groups:
+  // slot s after group (ks, i) = s * 2 SM / LPW.
+  auto compute = [&](int na, const char* stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[SM], bfr[SN];
 #pragma unroll
       for (int i = 0; i < SM; ++i) {
         if constexpr (A_KC) {
-          af[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * 32 * 64);
+          af[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * WM * 32 * 64);
         } else {
           const char* q = stage + a_mc[i] + 16 * ks * BM * 2;
           const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
@@ -531,12 +579,23 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         }
       }
 #pragma unroll
-      for (int i = 0; i < SM; ++i)
+      for (int i = 0; i < SM; ++i) {
+        if (i == 0 || i < na) {
 #pragma unroll
-        for (int j = 0; j < SN; ++j)
-          // Operands swapped: the result holds C^T fragments, so each lane
-          // owns one output row and runs of 4 consecutive output columns.
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < SN; ++j)
+            // Operands swapped: the result holds C^T fragments, so each lane
+            // owns one output row and runs of 4 consecutive output columns.
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < LPW; ++s2) {
+          if ((s2 * 2 * SM) / LPW == ks * SM + i) {
+            __builtin_amdgcn_sched_barrier(0);
+            dma_fire(s2);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
     }
   };
 
@@ -550,7 +609,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   };
 
   // ------------------------------------------------------ epilogue
-  // Lane owns output row  wrow0 + i*32 + l32  and columns
+  // Lane owns output row  m0 + sub_row(i) + l32  and columns
   // wcol0 + j*32 + 8*q + 4*khalf + {0..3} holding acc[i][j][4q..4q+3].
   char* slot = staging + wave * SLOT;  // this wave's staging slot (no other wave touches it)
   auto swap_halves = [](uint4 v) { return make_uint4(v.z, v.w, v.x, v.y); };
@@ -570,7 +629,6 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const __amdgpu_buffer_rsrc_t rsC2 = make_rsrc(p.C2, p.c2_bytes);  // SwiGLU pre-activation (0 bytes if absent)
 
   auto epilogue = [&](const Tile& t) __attribute__((always_inline)) {
-    const int wrow0 = t.m0 + wm * WTM;
     const int wcol0 = t.n0 + wn * WTN;
     const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
     // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
@@ -583,7 +641,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       // fp32 outputs (split-K partials, fp32 weight gradients): direct 16-byte stores.
 #pragma unroll
       for (int i = 0; i < SM; ++i) {
-        const int row = wrow0 + i * 32 + l32;
+        const int row = t.m0 + sub_row(i) + l32;
 #pragma unroll
         for (int j = 0; j < SN; ++j)
 #pragma unroll
@@ -614,7 +672,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     const int rr8 = lane >> 3, c8 = lane & 7;  // row-read lane mapping: row 8n + rr8, chunk c8
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
-      const int prow0 = wrow0 + i * 32;  // first output row of this pass
+      const int prow0 = t.m0 + sub_row(i);  // first output row of this pass
       // Output offsets of this pass's row reads and, when accumulating, the
       // existing gradient, loaded before the staging so that their latency
       // overlaps it.
@@ -704,7 +762,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   int cchunk = 0;
   int cj = 0, ck = 0;
   Tile ct;
-  bool c_active = false;
+  int n_act = 0;  // row sub-tiles of this wave that hold rows of the current tile (0: no MFMAs)
   // Sets the compute cursor on block tile j.  Tiles without k-steps (empty
   // groups of a weight gradient) are written out here directly: zeros, or
   // nothing when accumulating.  Returns false past the last tile.
@@ -729,10 +787,15 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     cj = j;
     ck = 0;
     const int row_limit = (MODE == MODE_MG) ? ct.re : p.M;
-    const int wrow0 = ct.m0 + wm * WTM, wcol0 = ct.n0 + wn * WTN;
-    // Waves whose rows or columns all lie outside the tile skip the MFMAs
-    // (they still take part in the DMA and the barriers).
-    c_active = wrow0 < row_limit && (EPI == EPI_SWIGLU_FWD || wcol0 < p.N);
+    const int wcol0 = ct.n0 + wn * WTN;
+    // Sub-tiles (and waves) whose rows or columns all lie outside the tile
+    // skip the MFMAs; every wave still takes part in the DMA and the barriers.
+    // Sub-tile i starts at tile row 32 (wm + WM i): i < n_act exactly when
+    // it starts below the tile's last row.
+    const int subs = (min(row_limit - ct.m0, BM) + 31) / 32;  // 32-row sub-tiles holding rows
+    int na = subs > wm ? (subs - wm + WM - 1) / WM : 0;
+    if (!(EPI == EPI_SWIGLU_FWD || wcol0 < p.N)) na = 0;
+    n_act = __builtin_amdgcn_readfirstlane(min(na, SM));
     return true;
   };
 
@@ -758,9 +821,15 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         wait_vmcnt<WAIT>();
       }
       barrier();
-      dma_issue(dstage);
+      dma_prepare(dstage);
+      if (n_act > 0) {
+        compute(n_act, ring + cstage * STAGE_BYTES);
+      } else {
+#pragma unroll
+        for (int j = 0; j < LPW; ++j) dma_fire(j);
+      }
+      dma_advance();
       dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
-      if (c_active) compute_stage(ring + cstage * STAGE_BYTES);
       cstage = cstage + 1 == STAGES ? 0 : cstage + 1;
       if (++ck == ct.nk) {
         epilogue(ct);
@@ -992,7 +1061,7 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
   if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, M * I * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
   p.c2_bytes = pre ? static_cast<uint32_t>(M * 2 * I * 2) : 0u;  // < a_bytes-range: checked below
   MOE_REQUIRE(M * 2 * I * 2 < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED, "swiglu fwd: pre-activation exceeds 2 GiB");
-  return launch<MODE_MG, true, EPI_SWIGLU_FWD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
+  return launch<MODE_MG, true, EPI_SWIGLU_FWD, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
 }
 
 extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t* offs, int64_t G, int64_t M, int64_t N,
@@ -1015,7 +1084,7 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
   p.ldc = N;
   p.stride_bg = N * K;
   if ((rc = set_bytes(p, M * K * 2, N * K * 2, M * N * 2, "moe_grouped_gemm_fwd"))) return rc;
-  return launch<MODE_MG, true, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_fwd");
+  return launch<MODE_MG, true, EPI_BF16, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_fwd");
 }
 
 // Router logits: f32 output, single group, no split.
@@ -1051,7 +1120,7 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   p.ldc = K;
   p.stride_bg = N * K;
   if ((rc = set_bytes(p, M * N * 2, N * K * 2, M * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
-  return launch<MODE_MG, false, EPI_BF16, BigTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
+  return launch<MODE_MG, false, EPI_BF16, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
 }
 
 extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down, const void* pre,
@@ -1080,7 +1149,7 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   p.stride_bg = H * I;
   if ((rc = set_bytes(p, M * H * 2, H * I * 2, (M * 2 * I - I) * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
   hipStream_t st = as_stream(stream);
-  if ((rc = launch<MODE_MG, false, EPI_BF16, BigTile>(p, st, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
+  if ((rc = launch<MODE_MG, false, EPI_BF16, ExpertTile>(p, st, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
   const int64_t chunks = M * I / 8;
   const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 4096));
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(grid), dim3(256), 0, st, static_cast<bf16_t*>(d_pre),
