@@ -99,15 +99,14 @@ struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int kThreads = 64 * WM * WN;
 };
-// Expert GEMMs over grouped rows (MG): 512-row tiles, so that an expert of up
-// to 512 rows is one m-tile and its weights stream through LDS once per
-// n-tile; 120 KiB ring + 32 KiB staging, 8 waves.
-using TallTile = TileCfg<512, 128, 32, 4, 2, 3>;
-// Expert weight gradients (KG): 128 KiB ring + 32 KiB staging, 8 waves.
+// Expert GEMMs and weight gradients: 128 KiB ring + 32 KiB staging, 8 waves.
 using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;
+// Expert GEMMs with narrow outputs: 512-row tiles, so that an expert of up to
+// 512 rows is one m-tile and its weights stream through LDS once per n-tile;
+// 120 KiB ring + 32 KiB staging, 8 waves.
+using TallTile = TileCfg<512, 128, 32, 4, 2, 3>;
 // Router GEMMs (N = E = 128): 64 KiB ring + 16 KiB staging, 4 waves.
 using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;
-using ExpertTile = TallTile;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
@@ -187,10 +186,10 @@ __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t of
 // exact.
 //
 // LDS layouts (per stage, per operand; 16-byte chunks, XOR-swizzled so that
-// the MFMA fragment reads are free of bank conflicts: gfx950 LDS serves
-// 256 bytes per clock, so the 16 lanes of a ds_read_b128 pass, or the 32
-// lanes of a ds_read_b64_tr_b16 pass, must touch 64 distinct banks):
-//   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ kc_swizzle(r)
+// the MFMA fragment reads are free of bank conflicts: gfx950 LDS has 64 banks
+// of 4 bytes, so the 16 lanes of a ds_read_b128 pass, or the 32 lanes of a
+// ds_read_b64_tr_b16 pass, must touch 64 distinct banks):
+//   K-contiguous operand  [R rows][BK k]:  chunk c of row r at slot c ^ kc_swizzle<BK>(r)
 //   M/N-contiguous operand [BK k][R cols]: chunk c of k-row kk at slot c ^ mc_swizzle(kk)
 // Each DMA instruction fills one contiguous 1 KiB block lane by lane (lane l
 // -> bytes 16l..16l+15), so a lane loads whichever global chunk belongs at
@@ -198,9 +197,14 @@ __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t of
 // fragments are two ds_read_b64_tr_b16, which turn a 4 (k) x 16 (n) patch read
 // by 16 lanes into 4 consecutive k per lane.
 
-// A ds_read_b128 pass reads one chunk of 16 consecutive rows: rows r and
-// r + 4k differ in bits 2-3, which move the chunk to another 16-byte bank group.
-__device__ __forceinline__ constexpr int kc_swizzle(int r) { return (r >> 2) & 3; }
+// A ds_read_b128 pass reads one chunk of 16 consecutive rows.  32-deep
+// k-tiles (64-byte rows, 4 rows per 256 bytes): rows r and r + 4k differ in
+// bits 2-3, which move the chunk to another 16-byte bank group.  64-deep
+// k-tiles (128-byte rows, 2 rows per 256 bytes): bits 1-3 do.
+template <int BK>
+__device__ __forceinline__ constexpr int kc_swizzle(int r) {
+  return BK == 32 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
 // A transpose-read pass reads 32 columns (4 chunks) of 4 consecutive k-rows:
 // k-row kk & 3 selects the 64-byte bank quarter (needs >= 16 chunks per k-row).
 __device__ __forceinline__ constexpr int mc_swizzle(int kk) { return 4 * (kk & 3); }
@@ -236,7 +240,10 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int WAIT = (STAGES - 2) * LPW;                     // DMA younger than the k-tile waited for
   constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
   constexpr int SLOT = 32 * WTN * 2;                           // staging bytes per wave (one 32-row pass)
-  static_assert(BK == 32, "swizzles and DMA mapping assume 32-deep k-tiles (4 chunks per K-contiguous row)");
+  static_assert(BK == 32 || BK == 64, "swizzles and DMA mapping cover 32- and 64-deep k-tiles");
+  constexpr int RB = BK * 2;      // bytes per K-contiguous row of a k-tile
+  constexpr int CPR = BK / 8;     // 16-byte chunks per K-contiguous row
+  constexpr int RPI = 64 / CPR;   // K-contiguous rows per DMA instruction
   static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
   static_assert(NI_A % NWAVES == 0 && NI_B % NWAVES == 0, "DMA instructions of each operand split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
@@ -384,8 +391,8 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     dma_lds[j] = __builtin_amdgcn_readfirstlane((is_a ? 0 : A_BYTES) + li * 1024);
     dma_col[j] = 0;
     if (is_a ? A_KC : B_KC) {
-      const int r = li * 16 + (lane >> 2);
-      dma_k[j] = ((lane & 3) ^ kc_swizzle(r)) * 8;
+      const int r = li * RPI + lane / CPR;
+      dma_k[j] = ((lane % CPR) ^ kc_swizzle<BK>(r)) * 8;
     } else {
       const int cpk = (is_a ? BM : BN) / 8;  // 16-byte chunks per k-row
       dma_k[j] = li * (64 / cpk) + lane / cpk;
@@ -428,8 +435,8 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       bool is_a;
       const int li = slot_inst(j2, is_a);
       if (is_a ? A_KC : B_KC) {
-        const int r = li * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ kc_swizzle(r);
+        const int r = li * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ kc_swizzle<BK>(r);
         bool ok;
         uint32_t row_bytes;
         if (is_a) {
@@ -512,15 +519,16 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   //
   // Each lane's byte offset within a stage is precomputed per fragment class;
   // a fragment address is the stage base plus a lane offset plus a constant.
-  // K-contiguous [R rows][4 chunks]: lane reads row (tile_row + l32), chunk
-  // 2 ks + khalf; fragment rows start on 32-row boundaries (row & 15 == l32 & 15).
+  // K-contiguous [R rows][CPR chunks]: lane reads row (tile_row + l32), chunk
+  // 2 ks + khalf; fragment rows start on 32-row boundaries, so the swizzle
+  // of row tile_row + l32 is that of l32.
   auto sub_row = [&](int i) { return (wm + WM * i) * 32; };
-  int a_kc[2], b_kc[2];
+  int a_kc[BK / 16], b_kc[BK / 16];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int lane_off = l32 * 64 + (((2 * ks + khalf) ^ kc_swizzle(l32)) << 4);
-    a_kc[ks] = sub_row(0) * 64 + lane_off;
-    b_kc[ks] = A_BYTES + wn * WTN * 64 + lane_off;
+  for (int ks = 0; ks < BK / 16; ++ks) {
+    const int lane_off = l32 * RB + (((2 * ks + khalf) ^ kc_swizzle<BK>(l32)) << 4);
+    a_kc[ks] = sub_row(0) * RB + lane_off;
+    b_kc[ks] = A_BYTES + wn * WTN * RB + lane_off;
   }
   // M/N-contiguous [BK k-rows][R cols] (transpose reads): lane = 16 q + i reads
   // k-rows 16 ks + 8 (q/2) + 4 h + i/4 and columns tile_col + 16 (q%2) + 4 (i%4).
@@ -551,7 +559,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // One k-tile of MFMAs over the first `na` row sub-tiles (the others hold no
   // rows of this tile; `na` is wave-uniform, so the guards are scalar
   // branches), with the prepared DMA slots fired between the MFMA groups:
-  // slot s after group (ks, i) = s * 2 SM / LPW.
+  // slot s after group (ks, i) = s * (BK / 16) SM / LPW.
   auto compute = [&](int na, const char* stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
@@ -559,7 +567,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
 #pragma unroll
       for (int i = 0; i < SM; ++i) {
         if constexpr (A_KC) {
-          af[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * WM * 32 * 64);
+          af[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * WM * 32 * RB);
         } else {
           const char* q = stage + a_mc[i] + 16 * ks * BM * 2;
           const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
@@ -570,7 +578,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
 #pragma unroll
       for (int j = 0; j < SN; ++j) {
         if constexpr (B_KC) {
-          bfr[j] = *reinterpret_cast<const bf16x8_t*>(stage + b_kc[ks] + j * 32 * 64);
+          bfr[j] = *reinterpret_cast<const bf16x8_t*>(stage + b_kc[ks] + j * 32 * RB);
         } else {
           const char* q = stage + b_mc[j] + 16 * ks * BN * 2;
           const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
@@ -589,7 +597,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         }
 #pragma unroll
         for (int s2 = 0; s2 < LPW; ++s2) {
-          if ((s2 * 2 * SM) / LPW == ks * SM + i) {
+          if ((s2 * (BK / 16) * SM) / LPW == ks * SM + i) {
             __builtin_amdgcn_sched_barrier(0);
             dma_fire(s2);
             __builtin_amdgcn_sched_barrier(0);
@@ -911,6 +919,18 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
   return launch_status(name);
 }
 
+// Expert GEMM over grouped rows.  256x256 tiles do the most MFMA work per
+// k-step of LDS traffic, but with few output columns their grid (about one
+// or two m-tiles per expert times the column tiles) ends in a poorly
+// balanced last round; 512x128 tiles give one m-tile per expert and twice
+// the column tiles.
+template <bool B_KCONTIG, int EPI>
+int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
+  const int out_cols = (EPI == EPI_SWIGLU_FWD) ? 2 * p.swiglu_I : p.N;
+  if (out_cols <= 1024) return launch<MODE_MG, B_KCONTIG, EPI, TallTile>(p, stream, name);
+  return launch<MODE_MG, B_KCONTIG, EPI, BigTile>(p, stream, name);
+}
+
 int check_common(const void* a, const void* b, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K) {
   MOE_REQUIRE(a && b, MOE_ERR_INVALID, "grouped gemm: null operand");
   MOE_REQUIRE(G >= 1 && G <= 4096, MOE_ERR_UNSUPPORTED, "grouped gemm: G=%lld outside [1,4096]", (long long)G);
@@ -1061,7 +1081,7 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
   if ((rc = set_bytes(p, M * H * 2, 2 * I * H * 2, M * I * 2, "moe_grouped_gemm_swiglu_fwd"))) return rc;
   p.c2_bytes = pre ? static_cast<uint32_t>(M * 2 * I * 2) : 0u;  // < a_bytes-range: checked below
   MOE_REQUIRE(M * 2 * I * 2 < kMaxRsrcBytes, MOE_ERR_UNSUPPORTED, "swiglu fwd: pre-activation exceeds 2 GiB");
-  return launch<MODE_MG, true, EPI_SWIGLU_FWD, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
+  return launch_expert<true, EPI_SWIGLU_FWD>(p, as_stream(stream), "moe_grouped_gemm_swiglu_fwd");
 }
 
 extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t* offs, int64_t G, int64_t M, int64_t N,
@@ -1084,7 +1104,7 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
   p.ldc = N;
   p.stride_bg = N * K;
   if ((rc = set_bytes(p, M * K * 2, N * K * 2, M * N * 2, "moe_grouped_gemm_fwd"))) return rc;
-  return launch<MODE_MG, true, EPI_BF16, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_fwd");
+  return launch_expert<true, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_fwd");
 }
 
 // Router logits: f32 output, single group, no split.
@@ -1120,7 +1140,7 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   p.ldc = K;
   p.stride_bg = N * K;
   if ((rc = set_bytes(p, M * N * 2, N * K * 2, M * K * 2, "moe_grouped_gemm_dgrad"))) return rc;
-  return launch<MODE_MG, false, EPI_BF16, ExpertTile>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
+  return launch_expert<false, EPI_BF16>(p, as_stream(stream), "moe_grouped_gemm_dgrad");
 }
 
 extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down, const void* pre,
@@ -1149,7 +1169,7 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   p.stride_bg = H * I;
   if ((rc = set_bytes(p, M * H * 2, H * I * 2, (M * 2 * I - I) * 2, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
   hipStream_t st = as_stream(stream);
-  if ((rc = launch<MODE_MG, false, EPI_BF16, ExpertTile>(p, st, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
+  if ((rc = launch_expert<false, EPI_BF16>(p, st, "moe_grouped_gemm_dgrad_swiglu_bwd"))) return rc;
   const int64_t chunks = M * I / 8;
   const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 4096));
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(grid), dim3(256), 0, st, static_cast<bf16_t*>(d_pre),
