@@ -15,7 +15,6 @@ namespace moe {
 
 constexpr int kCombThreads = 256;
 constexpr int kCombWaves = kCombThreads / kWave;
-constexpr int kMaxK = 16;
 
 __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
   f[0] = lo_bf16(v.x); f[1] = hi_bf16(v.x);
@@ -33,37 +32,36 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
   return o;
 }
 
+template <int KT>
 __global__ __launch_bounds__(kCombThreads) void combine_fwd_kernel(const bf16_t* __restrict__ y,
                                                                     const int32_t* __restrict__ pos_of_slot,
                                                                     const int32_t* __restrict__ n_valid_ptr,
                                                                     const float* __restrict__ scores, int T, int H,
                                                                     int k, bf16_t* __restrict__ out) {
+  constexpr int KM = Slots<KT>::KM;
   const int lane = threadIdx.x & (kWave - 1);
   const int n_valid = *n_valid_ptr;
   const int nchunk = H / 8;
   for (int t = blockIdx.x * kCombWaves + (threadIdx.x >> 6); t < T; t += gridDim.x * kCombWaves) {
-    int pos[kMaxK];
-    float w[kMaxK];
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-      pos[j] = n_valid;
-      w[j] = 0.0f;
-      if (j < k) {
-        pos[j] = pos_of_slot[static_cast<int64_t>(t) * k + j];
-        w[j] = scores ? scores[static_cast<int64_t>(t) * k + j] : 1.0f;
-      }
-    }
+    Slots<KT> sl;
+    sl.load(pos_of_slot, scores, t, k, n_valid);
     for (int c = lane; c < nchunk; c += kWave) {
+      // Every live slot's row load is issued before any is used; rows are
+      // added in slot order.
+      uint4 v[KM];
+#pragma unroll
+      for (int j = 0; j < KM; ++j)
+        if (KT || j < k) v[j] = reinterpret_cast<const uint4*>(y + static_cast<int64_t>(sl.pos[j]) * H)[c];
       float acc[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kMaxK; ++j) {
-        if (j < k && pos[j] < n_valid) {
+      for (int j = 0; j < KM; ++j) {
+        if (sl.ok[j]) {
           float f[8];
-          unpack8(reinterpret_cast<const uint4*>(y + static_cast<int64_t>(pos[j]) * H)[c], f);
+          unpack8(v[j], f);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += f[e] * w[j];
+          for (int e = 0; e < 8; ++e) acc[e] += f[e] * sl.w[j];
         }
       }
       reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * H)[c] = pack8(acc);
@@ -71,6 +69,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_fwd_kernel(const bf16_t*
   }
 }
 
+template <int KT>
 __global__ __launch_bounds__(kCombThreads) void combine_bwd_kernel(const bf16_t* __restrict__ d_out,
                                                                     const bf16_t* __restrict__ y,
                                                                     const int32_t* __restrict__ pos_of_slot,
@@ -78,39 +77,46 @@ __global__ __launch_bounds__(kCombThreads) void combine_bwd_kernel(const bf16_t*
                                                                     const float* __restrict__ scores, int T, int H,
                                                                     int k, bf16_t* __restrict__ d_y,
                                                                     float* __restrict__ d_scores) {
+  constexpr int KM = Slots<KT>::KM;
   const int lane = threadIdx.x & (kWave - 1);
   const int n_valid = *n_valid_ptr;
   const int nchunk = H / 8;
   for (int t = blockIdx.x * kCombWaves + (threadIdx.x >> 6); t < T; t += gridDim.x * kCombWaves) {
-    int pos[kMaxK];
-    float w[kMaxK], dot[kMaxK];
+    Slots<KT> sl;
+    sl.load(pos_of_slot, scores, t, k, n_valid);
+    // Slots without a row still get their (zero) gradient row written.
+    int dst_row[KM];
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-      pos[j] = n_valid;
-      w[j] = 0.0f;
-      dot[j] = 0.0f;
-      if (j < k) {
-        pos[j] = pos_of_slot[static_cast<int64_t>(t) * k + j];
-        w[j] = scores ? scores[static_cast<int64_t>(t) * k + j] : 1.0f;
-      }
+    for (int j = 0; j < KM; ++j) {
+      const bool live = KT ? true : j < k;
+      dst_row[j] = __builtin_amdgcn_readfirstlane(live ? pos_of_slot[static_cast<int64_t>(t) * k + j] : 0);
     }
+    float dot[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) dot[j] = 0.0f;
     for (int c = lane; c < nchunk; c += kWave) {
       float g[8];
       unpack8(reinterpret_cast<const uint4*>(d_out + static_cast<int64_t>(t) * H)[c], g);
+      uint4 v[KM];
+      if (d_scores) {
 #pragma unroll
-      for (int j = 0; j < kMaxK; ++j) {
-        if (j < k) {
-          uint4* dst = reinterpret_cast<uint4*>(d_y + static_cast<int64_t>(pos[j]) * H) + c;
-          if (pos[j] < n_valid) {
+        for (int j = 0; j < KM; ++j)
+          if (KT || j < k) v[j] = reinterpret_cast<const uint4*>(y + static_cast<int64_t>(sl.pos[j]) * H)[c];
+      }
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        if (KT || j < k) {
+          uint4* dst = reinterpret_cast<uint4*>(d_y + static_cast<int64_t>(dst_row[j]) * H) + c;
+          if (sl.ok[j]) {
             if (d_scores) {
               float f[8];
-              unpack8(reinterpret_cast<const uint4*>(y + static_cast<int64_t>(pos[j]) * H)[c], f);
+              unpack8(v[j], f);
 #pragma unroll
               for (int e = 0; e < 8; ++e) dot[j] += f[e] * g[e];
             }
             float o[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = g[e] * w[j];
+            for (int e = 0; e < 8; ++e) o[e] = g[e] * sl.w[j];
             *dst = pack8(o);
           } else {
             *dst = make_uint4(0, 0, 0, 0);
@@ -120,8 +126,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_bwd_kernel(const bf16_t*
     }
     if (d_scores) {
 #pragma unroll
-      for (int j = 0; j < kMaxK; ++j) {
-        if (j < k) {
+      for (int j = 0; j < KM; ++j) {
+        if (KT || j < k) {
           float s = wave_sum(dot[j]);
           if (lane == 0) d_scores[static_cast<int64_t>(t) * k + j] = s;
         }
@@ -138,9 +144,9 @@ int token_grid(int64_t T) {
 
 int check_combine(const void* rows, const int32_t* pos_of_slot, const int32_t* offsets, int64_t nb, int64_t T,
                   int64_t H, int64_t k, const void* out) {
-  MOE_REQUIRE(T >= 0 && T < (1ll << 31) && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0, MOE_ERR_INVALID,
+  MOE_REQUIRE(T >= 0 && T < (1ll << 31) && k >= 1 && k <= kMaxSlots && H > 0 && H % 8 == 0, MOE_ERR_INVALID,
               "combine: bad sizes T=%lld H=%lld k=%lld (H %% 8 == 0, 1 <= k <= %d)", (long long)T, (long long)H,
-              (long long)k, kMaxK);
+              (long long)k, kMaxSlots);
   MOE_REQUIRE(nb >= 1, MOE_ERR_INVALID, "combine: num_buckets must be >= 1");
   if (T == 0) return MOE_OK;
   MOE_REQUIRE(rows && pos_of_slot && offsets && out, MOE_ERR_INVALID, "combine: null pointer");
@@ -157,7 +163,7 @@ extern "C" int moe_combine_fwd(const void* y, const int32_t* pos_of_slot, const 
                                void* stream) {
   int rc = check_combine(y, pos_of_slot, offsets, num_buckets, T, H, k, out);
   if (rc || T == 0) return rc;
-  hipLaunchKernelGGL(combine_fwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
+  MOE_DISPATCH_K(k, combine_fwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
                      static_cast<const bf16_t*>(y), pos_of_slot, offsets + (num_buckets - 1), scores,
                      static_cast<int>(T), static_cast<int>(H), static_cast<int>(k), static_cast<bf16_t*>(out));
   return launch_status("moe_combine_fwd");
@@ -169,7 +175,7 @@ extern "C" int moe_combine_bwd(const void* d_out, const void* y, const int32_t* 
   int rc = check_combine(d_out, pos_of_slot, offsets, num_buckets, T, H, k, d_y);
   if (rc || T == 0) return rc;
   MOE_REQUIRE(!d_scores || (y && aligned16(y)), MOE_ERR_INVALID, "combine bwd: d_scores needs y");
-  hipLaunchKernelGGL(combine_bwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
+  MOE_DISPATCH_K(k, combine_bwd_kernel, dim3(token_grid(T)), dim3(kCombThreads), 0, as_stream(stream),
                      static_cast<const bf16_t*>(d_out), static_cast<const bf16_t*>(y), pos_of_slot,
                      offsets + (num_buckets - 1), scores, static_cast<int>(T), static_cast<int>(H),
                      static_cast<int>(k), static_cast<bf16_t*>(d_y), d_scores);

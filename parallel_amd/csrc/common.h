@@ -21,16 +21,15 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 
-// Round-to-nearest-even float -> bf16 (NaN stays NaN), the rounding torch uses.
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<bf16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
-}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even float -> bf16 (NaN stays NaN), the rounding torch
+// uses; gfx950 converts in hardware (v_cvt_pk_bf16_f32, two values at once).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
@@ -118,6 +117,46 @@ int launch_status(const char* what);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kMaxSlots = 16;  // top-k slots per token handled by the k-way kernels
+
+// A token's slots, read once per wave into wave-uniform registers: the row
+// position (0 for a slot without a row, whose loads are then discarded), the
+// live flag and the routing weight.  KT > 0 fixes the slot count at compile
+// time; KT == 0 takes k <= kMaxSlots at run time.
+template <int KT>
+struct Slots {
+  static constexpr int KM = KT ? KT : kMaxSlots;
+  int pos[KM];
+  bool ok[KM];
+  float w[KM];
+  __device__ __forceinline__ void load(const int32_t* pos_of_slot, const float* scores, int64_t t, int k,
+                                       int n_valid) {
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      const bool live = KT ? true : j < k;
+      int p = live ? pos_of_slot[t * k + j] : n_valid;
+      float wj = (live && scores) ? scores[t * k + j] : 1.0f;
+      p = __builtin_amdgcn_readfirstlane(p);
+      wj = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, wj)));
+      ok[j] = live && p < n_valid;
+      pos[j] = ok[j] ? p : 0;
+      w[j] = wj;
+    }
+  }
+};
+
+// Launches KERNEL<k> for the common top-k values (compile-time slot count)
+// and KERNEL<0> (run-time k) otherwise.
+#define MOE_DISPATCH_K(k, KERNEL, ...)                                      \
+  switch (k) {                                                              \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;              \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;              \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;              \
+    case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;              \
+    case 8: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;              \
+    default: hipLaunchKernelGGL(KERNEL<0>, __VA_ARGS__); break;             \
+  }
 
 }  // namespace moe
 

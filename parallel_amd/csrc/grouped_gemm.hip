@@ -73,7 +73,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g * sigmoid(g), with the hardware exp and reciprocal (1 ulp).
+__device__ __forceinline__ float sigmoid_f(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
 // Total tiles over all groups, sum_g n_mult * ceil(cnt_g / BM) (wave-uniform).
 template <int BM>
@@ -1040,7 +1042,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(bf16_t* __restrict__ d_
         const float d = h ? hi_bf16(dw[e]) : lo_bf16(dw[e]);
         const float g = h ? hi_bf16(gw[e]) : lo_bf16(gw[e]);
         const float u = h ? hi_bf16(uw[e]) : lo_bf16(uw[e]);
-        const float sg = 1.0f / (1.0f + __expf(-g));
+        const float sg = sigmoid_f(g);
         du2[h] = d * bf16_to_f32(f32_to_bf16(g * sg));
         dg2[h] = bf16_to_f32(f32_to_bf16(d * u)) * sg * (1.0f + g * (1.0f - sg));
       }

@@ -158,7 +158,16 @@ __global__ __launch_bounds__(kPermThreads) void gather_rows_kernel(const bf16_t*
     uint4* dst = reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos) * H);
     if (pos < n_valid) {
       const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<int64_t>(perm[pos] / k) * H);
-      for (int c = lane; c < nchunk; c += kWave) dst[c] = src[c];
+      // Four 16-byte chunks per lane in flight before their stores.
+      int c = lane;
+      for (; c + 3 * kWave < nchunk; c += 4 * kWave) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = src[c + u * kWave];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dst[c + u * kWave] = v[u];
+      }
+      for (; c < nchunk; c += kWave) dst[c] = src[c];
     } else {
       for (int c = lane; c < nchunk; c += kWave) dst[c] = make_uint4(0, 0, 0, 0);
     }
@@ -178,40 +187,47 @@ __global__ void dispatch_meta_kernel(const int64_t* __restrict__ ids, const floa
   }
 }
 
-// d_hidden[t] = sum_j d_permuted[pos_of_slot[t*k+j]] (+ d_add[t]); one wave per token.
+// d_hidden[t] = sum_j d_permuted[pos_of_slot[t*k+j]] (+ d_add[t]); one wave
+// per token.  Every live slot's row load is issued before any is added
+// (slot order, then d_add); KT as in Slots.
+template <int KT>
 __global__ __launch_bounds__(kPermThreads) void permute_bwd_kernel(const bf16_t* __restrict__ dperm,
                                                                     const int32_t* __restrict__ pos_of_slot,
                                                                     const int32_t* __restrict__ n_valid_ptr, int T,
                                                                     int H, int k, const bf16_t* __restrict__ d_add,
                                                                     bf16_t* __restrict__ dh) {
+  constexpr int KM = Slots<KT>::KM;
   const int lane = threadIdx.x & (kWave - 1);
   const int n_valid = *n_valid_ptr;
   const int nchunk = H / 8;
   for (int t = blockIdx.x * (kPermThreads / kWave) + (threadIdx.x >> 6); t < T;
        t += gridDim.x * (kPermThreads / kWave)) {
-    int pos[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) pos[j] = (j < k) ? pos_of_slot[static_cast<int64_t>(t) * k + j] : n_valid;
+    Slots<KT> sl;
+    sl.load(pos_of_slot, nullptr, t, k, n_valid);
     for (int c = lane; c < nchunk; c += kWave) {
+      uint4 v[KM];
+#pragma unroll
+      for (int j = 0; j < KM; ++j)
+        if (KT || j < k) v[j] = reinterpret_cast<const uint4*>(dperm + static_cast<int64_t>(sl.pos[j]) * H)[c];
+      uint4 va = make_uint4(0, 0, 0, 0);
+      if (d_add) va = reinterpret_cast<const uint4*>(d_add + static_cast<int64_t>(t) * H)[c];
       float acc[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (j < k && pos[j] < n_valid) {
-          uint4 v = reinterpret_cast<const uint4*>(dperm + static_cast<int64_t>(pos[j]) * H)[c];
-          acc[0] += lo_bf16(v.x); acc[1] += hi_bf16(v.x);
-          acc[2] += lo_bf16(v.y); acc[3] += hi_bf16(v.y);
-          acc[4] += lo_bf16(v.z); acc[5] += hi_bf16(v.z);
-          acc[6] += lo_bf16(v.w); acc[7] += hi_bf16(v.w);
+      for (int j = 0; j < KM; ++j) {
+        if (sl.ok[j]) {
+          acc[0] += lo_bf16(v[j].x); acc[1] += hi_bf16(v[j].x);
+          acc[2] += lo_bf16(v[j].y); acc[3] += hi_bf16(v[j].y);
+          acc[4] += lo_bf16(v[j].z); acc[5] += hi_bf16(v[j].z);
+          acc[6] += lo_bf16(v[j].w); acc[7] += hi_bf16(v[j].w);
         }
       }
       if (d_add) {
-        uint4 v = reinterpret_cast<const uint4*>(d_add + static_cast<int64_t>(t) * H)[c];
-        acc[0] += lo_bf16(v.x); acc[1] += hi_bf16(v.x);
-        acc[2] += lo_bf16(v.y); acc[3] += hi_bf16(v.y);
-        acc[4] += lo_bf16(v.z); acc[5] += hi_bf16(v.z);
-        acc[6] += lo_bf16(v.w); acc[7] += hi_bf16(v.w);
+        acc[0] += lo_bf16(va.x); acc[1] += hi_bf16(va.x);
+        acc[2] += lo_bf16(va.y); acc[3] += hi_bf16(va.y);
+        acc[4] += lo_bf16(va.z); acc[5] += hi_bf16(va.z);
+        acc[6] += lo_bf16(va.w); acc[7] += hi_bf16(va.w);
       }
       uint4 o;
       o.x = pack_bf16x2(acc[0], acc[1]);
@@ -304,7 +320,7 @@ extern "C" int moe_permute_bwd(const void* d_permuted, const int32_t* pos_of_slo
   MOE_REQUIRE(d_permuted && pos_of_slot && offsets && d_hidden, MOE_ERR_INVALID, "permute bwd: null pointer");
   MOE_REQUIRE(aligned16(d_permuted) && aligned16(d_hidden) && (!d_add || aligned16(d_add)), MOE_ERR_INVALID,
               "permute bwd: buffers must be 16-byte aligned");
-  hipLaunchKernelGGL(permute_bwd_kernel, dim3(row_grid(T)), dim3(kPermThreads), 0, as_stream(stream),
+  MOE_DISPATCH_K(k, permute_bwd_kernel, dim3(row_grid(T)), dim3(kPermThreads), 0, as_stream(stream),
                      static_cast<const bf16_t*>(d_permuted), pos_of_slot, offsets + (num_buckets - 1),
                      static_cast<int>(T), static_cast<int>(H), static_cast<int>(k),
                      static_cast<const bf16_t*>(d_add), static_cast<bf16_t*>(d_hidden));

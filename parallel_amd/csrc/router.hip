@@ -117,8 +117,17 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
     v[j] = -INFINITY;
     if (j < npl && e < E) {
       const float* src = partials + static_cast<int64_t>(t) * E + e;
+      // Loads in batches of 8 (independent), added in split order.
       float acc = 0.0f;
-      for (int sp = 0; sp < splits; ++sp) acc += src[sp * plane];
+      int sp = 0;
+      for (; sp + 8 <= splits; sp += 8) {
+        float q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = src[(sp + u) * plane];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += q[u];
+      }
+      for (; sp < splits; ++sp) acc += src[sp * plane];
       if (bias) acc += bias[e];
       v[j] = acc;
       logits[static_cast<int64_t>(t) * E + e] = acc;
@@ -231,11 +240,11 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
 
 // ------------------------------------------------------------------ aux loss
 
-constexpr int kAuxBlocksMax = 1024;
-constexpr int kAuxTokensPerWave = 4;
+constexpr int kAuxBlocksMax = 1024;  // per-block partial rows (a wave takes one token at a time)
+constexpr int kAuxGroups = 16;       // row groups of the partial reduction
 
 int aux_blocks(int64_t T) {
-  int64_t b = (T + kRouterWaves * kAuxTokensPerWave - 1) / (kRouterWaves * kAuxTokensPerWave);
+  int64_t b = (T + kRouterWaves - 1) / kRouterWaves;
   if (b < 1) b = 1;
   return static_cast<int>(b < kAuxBlocksMax ? b : kAuxBlocksMax);
 }
@@ -295,32 +304,49 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_partial_kernel(const
   }
 }
 
-// Column sums of the per-block partials, fixed order: 64 entries per block,
-// wave w adds blocks w, w+4, ...; the 4 wave sums are combined in wave order.
+// Column sums of the per-block partials in kAuxGroups row groups, fixed
+// order: block (x, g) sums entries 64x .. 64x+63 over the rows of group g
+// (wave w adds rows w, w+4, ... of the group; the 4 wave sums are combined in
+// wave order) into sums[g][entry].
 __global__ __launch_bounds__(256) void aux_reduce_kernel(const float* __restrict__ ws, int nblk, int n,
                                                          float* __restrict__ sums) {
   __shared__ float part[4][64];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int entry = blockIdx.x * 64 + lane;
+  const int g = blockIdx.y;
+  const int per = (nblk + kAuxGroups - 1) / kAuxGroups;
+  const int r0 = g * per, r1 = min(nblk, r0 + per);
   float acc = 0.0f;
   if (entry < n) {
-#pragma unroll 4
-    for (int b = wave; b < nblk; b += 4) acc += ws[static_cast<int64_t>(b) * n + entry];
+#pragma unroll 8
+    for (int b = r0 + wave; b < r1; b += 4) acc += ws[static_cast<int64_t>(b) * n + entry];
   }
   part[wave][lane] = acc;
   __syncthreads();
-  if (wave == 0 && entry < n) sums[entry] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+  if (wave == 0 && entry < n)
+    sums[static_cast<int64_t>(g) * n + entry] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
 }
 
-// sums = (P_0..P_{E-1}, c_0..c_{E-1}, W) -> stats = (c, W), aux = E * sum_e (c_e/W)(P_e/W).
+// sums[g] = (P_0..P_{E-1}, c_0..c_{E-1}, W) per row group, added in group
+// order -> stats = (c, W), aux = E * sum_e (c_e/W)(P_e/W).
 __global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restrict__ sums, int E,
                                                              float* __restrict__ stats, float* __restrict__ aux) {
   __shared__ float terms[1024];
   const int tid = threadIdx.x;
-  const float W = sums[2 * E];
+  const int n = 2 * E + 1;
+  auto total = [&](int entry) {
+    float q[kAuxGroups];
+#pragma unroll
+    for (int g = 0; g < kAuxGroups; ++g) q[g] = sums[static_cast<int64_t>(g) * n + entry];
+    float s = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kAuxGroups; ++g) s += q[g];
+    return s;
+  };
+  const float W = total(2 * E);
   float term = 0.0f;
   if (tid < E) {
-    float P = sums[tid], C = sums[E + tid];
+    float P = total(tid), C = total(E + tid);
     stats[tid] = C;
     term = (C / W) * (P / W);
   }
@@ -419,7 +445,7 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
 
 extern "C" size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E) {
   if (T < 0 || E < 1) return 0;
-  return static_cast<size_t>(aux_blocks(T) + 1) * static_cast<size_t>(2 * E + 1) * sizeof(float);
+  return static_cast<size_t>(aux_blocks(T) + kAuxGroups) * static_cast<size_t>(2 * E + 1) * sizeof(float);
 }
 
 extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, int64_t T, int64_t E, int64_t k,
@@ -438,7 +464,8 @@ extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, 
   if (rc) return rc;
   const int n = static_cast<int>(2 * E + 1);
   float* sums = ws + static_cast<int64_t>(nblk) * n;
-  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64), dim3(256), 0, as_stream(stream), ws, nblk, n, sums);
+  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64, kAuxGroups), dim3(256), 0, as_stream(stream), ws, nblk,
+                     n, sums);
   rc = launch_status("moe_aux_loss_fwd(reduce)");
   if (rc) return rc;
   hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, as_stream(stream), sums, static_cast<int>(E), stats,
