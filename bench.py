@@ -113,20 +113,19 @@ _GEMM_ORDER = {
 def tag_dispatches(names):
     """Bench timer tag of each kernel dispatch, given kernel names in dispatch order.
 
-    The expert GEMMs are the grouped_gemm instantiations sharing the tile
-    configuration of the SwiGLU forward (epilogue 2); an instantiation that
-    serves two entry points is told apart by its occurrence order (each step
-    launches them in a fixed order)."""
+    The expert GEMMs are the grouped_gemm instantiations with tiles of 256 or
+    more rows (the router GEMMs use 128-row tiles); entry points that share a
+    (mode, operand layout, epilogue) signature are told apart by their
+    occurrence order (each step launches them in a fixed order)."""
     import re
 
     parsed = [re.search(_GEMM_RE, n) for n in names]
-    expert_cfg = next((m[4] for m in parsed if m and m[3] == "2"), None)
     seen = {}
     tags = []
     for n, m in zip(names, parsed):
         if m:
             key = (int(m[1]), m[2] == "true", int(m[3]))
-            if m[4] == expert_cfg and key in _GEMM_ORDER:
+            if int(m[4].split(",")[0]) >= 256 and key in _GEMM_ORDER:
                 order = _GEMM_ORDER[key]
                 i = seen.get(key, 0)
                 seen[key] = i + 1

@@ -7,19 +7,21 @@
 // MG = groups partition the rows of the activation operand (variable M per
 // expert), KG = groups partition the reduction (variable K per expert).
 //
-// Tiling: WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of 32x32
-// MFMA sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators).  The expert
-// GEMMs use 256x256 tiles on 8 waves (two waves per SIMD, one workgroup per
-// CU); the small router GEMMs use 128x128 on 4 waves.  Operands move from HBM
-// to LDS by DMA (buffer_load_dwordx4 ... lds, no register staging) into a
-// 4-deep ring of 32-deep k-tiles, so three k-tiles of loads are in flight
-// while one is multiplied.  Each operand keeps its HBM layout in LDS (XOR
-// swizzled): K-contiguous fragments are ds_read_b128, M/N-contiguous ones
-// (weights in the input gradient, both operands of the weight gradient) are
-// ds_read_b64_tr_b16 transpose reads.  Buffer loads read zero past the
-// resource size, so ragged rows and the K tail need no branches.  Sub-tiles
-// of a wave that lie wholly outside the valid rows/columns skip their
-// fragment reads and MFMAs (the last M tile of an expert is usually short).
+// Tiling: WM x WN waves; each wave owns (BM/WM) x (BN/WN) of 32x32 MFMA
+// sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators), its row sub-tiles
+// interleaved with the other wave rows'.  The expert GEMMs use 256x256 tiles
+// (512x128 when the output is at most 1024 columns wide) on 8 waves (two waves
+// per SIMD, one workgroup per CU); the small router GEMMs use 128x128 on 4
+// waves.  Operands move from HBM to LDS by DMA (buffer_load_dwordx4 ... lds,
+// no register staging) into a 3- or 4-deep ring of 32-deep k-tiles, so two
+// or three k-tiles of loads are in flight while one is multiplied; each wave
+// fires its share of a k-tile's DMA between its MFMA groups.  Each operand
+// keeps its HBM layout in LDS (XOR swizzled): K-contiguous fragments are
+// ds_read_b128, M/N-contiguous ones (weights in the input gradient, both
+// operands of the weight gradient) are ds_read_b64_tr_b16 transpose reads.
+// Buffer loads read zero past the resource size, so ragged rows and the K
+// tail need no branches.  Row sub-tiles that lie wholly outside the valid
+// rows skip their MFMAs (the last M tile of an expert is usually short).
 //
 // Tiles are mapped to groups on the device from the `offs` cumsum (no host
 // sync).  The logical tile order is group-major, then n-tile, then m-tile, so

@@ -116,3 +116,25 @@ def test_workload_shapes():
     assert c2.gemm_flops() == pytest.approx(9.277e11, rel=1e-3)
     assert WORKLOADS["c4"].gemm_flops() == pytest.approx(3.711e12, rel=1e-3)
     assert WORKLOADS["c5"].gemm_flops() == pytest.approx(7.422e12, rel=1e-3)
+
+
+def test_bench_tags_kernel_dispatches_by_entry_point():
+    """rocprofv3 kernel names of one step -> the bench's per-entry-point tags."""
+    import bench
+
+    g = "void moe::grouped_gemm_kernel<{}, {}, {}, moe::TileCfg<{}> >(moe::GemmParams)"
+    big, tall, small = "256, 256, 32, 2, 4, 4", "512, 128, 32, 4, 2, 3", "128, 128, 32, 2, 2, 4"
+    names = [
+        g.format(0, "true", 1, small), "moe::router_reduce_topk_kernel(float const*)",
+        g.format(0, "true", 2, big), g.format(0, "true", 0, big), "void moe::combine_fwd_kernel<8>(unsigned short const*)",
+        "void moe::combine_bwd_kernel<8>(unsigned short const*)",
+        g.format(0, "false", 0, tall), "moe::swiglu_bwd_kernel(unsigned short*)", g.format(1, "false", 4, big),
+        g.format(0, "false", 0, big), g.format(1, "false", 4, big),
+        "void moe::permute_bwd_kernel<8>(unsigned short const*)",
+        g.format(1, "false", 4, small), g.format(0, "false", 0, small),
+    ]
+    assert bench.tag_dispatches(names) == [
+        "router_fwd", "router_fwd", "up_fwd", "down_fwd", "combine_fwd", "combine_bwd",
+        "down_dgrad", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad", "permute_bwd",
+        "router_gemm_bwd", "router_gemm_bwd",
+    ]
