@@ -8,6 +8,7 @@ and as drop-ins for the reference's interfaces.
 """
 
 from .aux_loss import load_balancing_loss_func, sequence_parallel_load_balancing_loss
+from .checkpoint import MoeLayerWeights, load_moe_layer
 from .expert_parallel import (
     ExpertPartition,
     ReplicatedTokenExpertParallel,
@@ -32,12 +33,14 @@ __all__ = [
     "ExpertPartition",
     "Experts",
     "MoeConfig",
+    "MoeLayerWeights",
     "ReplicatedTokenExpertParallel",
     "SequenceParallelExpertParallel",
     "SparseMoeBlock",
     "TokenDispatcher",
     "TopKRouter",
     "load_balancing_loss_func",
+    "load_moe_layer",
     "local_expert_range",
     "mi355x_experts_forward",
     "register_experts_implementation",
