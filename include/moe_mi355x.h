@@ -116,6 +116,39 @@ int moe_aux_loss_bwd(const float* logits, const float* token_weight,
                      const float* stats, const float* d_aux, int64_t T,
                      int64_t E, float* d_logits, int accumulate, void* stream);
 
+/* ------------------------------------- the step before: norm -> router -> aux */
+
+/* RMSNorm of the MoE block's input (post_attention_layernorm), per row:
+ *   r = rsqrt(mean(h^2) + eps) in fp32;  x = bf16(gamma * bf16(h * r));  rstd[t] = r.
+ * h, gamma, x bf16 (16-byte aligned); H a multiple of 8, H <= 4096.
+ * Replaces Qwen3MoeRMSNorm.forward (TF/models/qwen3_moe/modeling_qwen3_moe.py:294-299)
+ * as applied before the MoE block (:345). */
+int moe_rmsnorm_fwd(const void* h, const void* gamma, int64_t T, int64_t H,
+                    float eps, void* x, float* rstd, void* stream);
+
+/* Backward of moe_rmsnorm_fwd (autograd of :294-299): with g = bf16(dx + dx2)
+ * (dx2 may be NULL; autograd adds the router's and the experts' gradients of
+ * x in bf16), dhs = bf16(g * gamma):
+ *   dh = bf16(r * dhs - (r^3 / H) * h * sum_j dhs_j h_j),
+ *   dgamma = bf16(sum_t bf16(g * bf16(h * r)))  (fixed-order column sums). */
+size_t moe_rmsnorm_bwd_workspace_bytes(int64_t T, int64_t H);
+int moe_rmsnorm_bwd(const void* dx, const void* dx2, const void* h,
+                    const void* gamma, const float* rstd, int64_t T, int64_t H,
+                    void* dh, void* dgamma, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* moe_router_fwd plus the Switch aux loss of moe_aux_loss_fwd (same aux and
+ * stats outputs, token_weight as there) from the router's own softmax and
+ * top-k, where the reference recomputes both from the logits
+ * (TF/models/qwen3_moe/modeling_qwen3_moe.py:550-552 inside load_balancing_loss_func
+ * :514-593).  T >= 1. */
+size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
+int moe_router_aux_fwd(const void* x, const void* wr, const float* logit_bias,
+                       const float* token_weight, float* logits, float* scores,
+                       int64_t* indices, int64_t T, int64_t H, int64_t E,
+                       int64_t k, int norm_topk_prob, float* aux, float* stats,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ----------------------------------------------------------------- permute */
 
 /* Stable counting sort of S = T*k routed slots by bucket = ids[s] / divisor

@@ -14,6 +14,8 @@ It restates, on the CPU, the reference path's arithmetic:
                      parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280
   * EP ownership     parallel/parallel/engine/model_parallel/expert_parallel.py:12-60
   * token dispatch   parallel/parallel/engine/model_parallel/token_dispatch.py:86-174
+  * block-input norm TF/models/qwen3_moe/modeling_qwen3_moe.py:294-299 (Qwen3MoeRMSNorm, the
+                     post_attention_layernorm applied before the MoE block at :345)
 where TF/ is transformers (the reference pins 5.14.1, uv.lock:2274-2275; the
 5.15.0 installed here is what the golden vectors were generated with).
 Integer work (sort keys, permutations, counts, splits) is numpy; floating
@@ -34,6 +36,29 @@ from __future__ import annotations
 import numpy as np
 import torch
 import torch.nn.functional as F
+
+# ----------------------------------------------------------------- norm
+
+
+def rmsnorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen3MoeRMSNorm.forward (modeling_qwen3_moe.py:294-299): fp32 statistics,
+    then weight * hs.to(input dtype) in the input dtype (autograd-capable)."""
+    input_dtype = hidden.dtype
+    hs = hidden.to(torch.float32)
+    variance = hs.pow(2).mean(-1, keepdim=True)
+    hs = hs * torch.rsqrt(variance + eps)
+    return weight * hs.to(input_dtype)
+
+
+def norm_router_aux(hidden, norm_weight, router_weight, top_k, *, eps, norm_topk_prob, attention_mask=None):
+    """The step before the MoE block: post_attention_layernorm (:345), the router
+    (:258-267, fp32 logits) and the aux loss over the same logits (:514-593)."""
+    x = rmsnorm(hidden, norm_weight, eps)
+    logits = router_logits(x.reshape(-1, x.shape[-1]), router_weight)
+    scores, indices = topk_softmax(logits, top_k, norm_topk_prob)
+    aux = load_balancing_loss((logits,), router_weight.shape[0], top_k, attention_mask)
+    return x, logits, scores, indices, aux
+
 
 # ----------------------------------------------------------------- router
 

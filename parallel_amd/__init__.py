@@ -9,6 +9,7 @@ and as drop-ins for the reference's interfaces.
 
 from .aux_loss import load_balancing_loss_func, sequence_parallel_load_balancing_loss
 from .checkpoint import MoeLayerWeights, load_moe_layer
+from .norm_router import norm_router_aux
 from .expert_parallel import (
     ExpertPartition,
     ReplicatedTokenExpertParallel,
@@ -41,6 +42,7 @@ __all__ = [
     "TopKRouter",
     "load_balancing_loss_func",
     "load_moe_layer",
+    "norm_router_aux",
     "local_expert_range",
     "mi355x_experts_forward",
     "register_experts_implementation",

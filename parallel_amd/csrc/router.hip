@@ -102,15 +102,25 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_fwd_kernel(c
 }
 
 // logits[t] = sum_s partials[s][t] (+ bias), then the top-k softmax of that row.
+// With aux_ws, also the aux-loss partials of the block's 4 tokens from the
+// same softmax and selection (the layout and arithmetic of aux_partial_kernel).
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kernel(
     const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
-    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k, int norm) {
+    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k, int norm,
+    const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
+  __shared__ float part[kRouterWaves][2 * 1024 + 1];
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t >= T) return;
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * kRouterWaves + wave;
+  if (t >= T && !aux_ws) return;
   const int npl = (E + kWave - 1) / kWave;
   const int64_t plane = static_cast<int64_t>(T) * E;
   float v[kMaxPerLane];
+  float P[kMaxPerLane], C[kMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kMaxPerLane; ++j) P[j] = C[j] = 0.0f;
+  float W = 0.0f;
+  if (t < T) {
 #pragma unroll
   for (int j = 0; j < kMaxPerLane; ++j) {
     int e = lane + j * kWave;
@@ -151,6 +161,44 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
     if (r < k && lane == r) {
       scores[static_cast<int64_t>(t) * k + r] = norm ? pv[r] / tot : pv[r];
       indices[static_cast<int64_t>(t) * k + r] = sel[r];
+    }
+  }
+  if (aux_ws) {
+    const float w = token_weight ? token_weight[t] : 1.0f;
+    W = w;
+    const float inv_sum = 1.0f / st.sum;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+      int e = lane + j * kWave;
+      if (j < npl && e < E) {
+        P[j] = w * (expf(v[j] - st.max) * inv_sum);
+        float cnt = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kMaxTopK; ++r)
+          if (r < k && sel[r] == e) cnt += 1.0f;
+        C[j] = w * cnt;
+      }
+    }
+  }
+  }  // t < T
+  if (aux_ws) {
+    // The block's 4 tokens, added in wave order (aux_partial_kernel's sums
+    // start from zero, so each wave's term is 0 + term).
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+      int e = lane + j * kWave;
+      if (j < npl && e < E) {
+        part[wave][e] = 0.0f + P[j];
+        part[wave][E + e] = 0.0f + C[j];
+      }
+    }
+    if (lane == 0) part[wave][2 * E] = 0.0f + W;
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * E + 1; i += blockDim.x) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kRouterWaves; ++w) s += part[w][i];
+      aux_ws[static_cast<int64_t>(blockIdx.x) * (2 * E + 1) + i] = s;
     }
   }
 }
@@ -531,8 +579,53 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
   int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
   hipLaunchKernelGGL(router_reduce_topk_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits,
                      logit_bias, logits, scores, indices, static_cast<int>(T), static_cast<int>(E),
-                     static_cast<int>(k), norm_topk_prob ? 1 : 0);
+                     static_cast<int>(k), norm_topk_prob ? 1 : 0, nullptr, nullptr);
   return launch_status("moe_router_fwd(reduce+topk)");
+}
+
+extern "C" size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
+  if (T < 0 || H < 1 || E < 1) return 0;
+  const int64_t blocks = (T + kRouterWaves - 1) / kRouterWaves;
+  const size_t aux = static_cast<size_t>(blocks + kAuxGroups) * static_cast<size_t>(2 * E + 1) * sizeof(float);
+  return moe_router_fwd_workspace_bytes(T, H, E) + aux;
+}
+
+extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* logit_bias, const float* token_weight,
+                                  float* logits, float* scores, int64_t* indices, int64_t T, int64_t H, int64_t E,
+                                  int64_t k, int norm_topk_prob, float* aux, float* stats, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int rc = check_router(T, E, k);
+  if (rc) return rc;
+  MOE_REQUIRE(x && wr && logits && scores && indices && aux && stats, MOE_ERR_INVALID,
+              "router aux fwd: null pointer");
+  MOE_REQUIRE(T >= 1, MOE_ERR_INVALID, "router aux fwd: the aux loss needs at least one token");
+  MOE_REQUIRE(H > 0 && H % 8 == 0 && E % 8 == 0 && aligned16(x) && aligned16(wr), MOE_ERR_UNSUPPORTED,
+              "router aux fwd: H (%lld) and E (%lld) must be multiples of 8 with 16-byte aligned operands",
+              (long long)H, (long long)E);
+  const size_t need = moe_router_aux_fwd_workspace_bytes(T, H, E);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "router aux fwd: workspace %zu < %zu bytes",
+              workspace_bytes, need);
+  int splits, k_chunk;
+  router_split(T, H, E, splits, k_chunk);
+  float* partials = static_cast<float*>(workspace);
+  float* aux_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + moe_router_fwd_workspace_bytes(T, H, E));
+  hipStream_t st = as_stream(stream);
+  rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
+                              static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
+  if (rc) return rc;
+  const int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
+  hipLaunchKernelGGL(router_reduce_topk_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits,
+                     logit_bias, logits, scores, indices, static_cast<int>(T), static_cast<int>(E),
+                     static_cast<int>(k), norm_topk_prob ? 1 : 0, token_weight, aux_ws);
+  rc = launch_status("moe_router_aux_fwd(reduce+topk+aux partials)");
+  if (rc) return rc;
+  const int n = static_cast<int>(2 * E + 1);
+  float* sums = aux_ws + static_cast<int64_t>(blocks) * n;
+  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64, kAuxGroups), dim3(256), 0, st, aux_ws, blocks, n, sums);
+  rc = launch_status("moe_router_aux_fwd(reduce)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, st, sums, static_cast<int>(E), stats, aux);
+  return launch_status("moe_router_aux_fwd(finalize)");
 }
 
 extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {

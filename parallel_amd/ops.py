@@ -12,6 +12,8 @@ Ops (namespace ``parallel_amd``):
   experts_fwd / experts_bwd        permute -> SwiGLU grouped GEMMs -> combine
   dispatch_fwd / dispatch_bwd      owner-rank sort for TokenDispatcher
   combine_rows_fwd / _bwd          gather-form index_add back to source tokens
+  rmsnorm_fwd / rmsnorm_bwd        post_attention_layernorm of the block input (+ backward)
+  router_aux_fwd                   router_fwd plus the aux loss from the same top-k
 """
 
 from __future__ import annotations
@@ -221,6 +223,122 @@ def _aux_backward(ctx, d_aux, _d_stats):
 
 
 aux_loss_fwd.register_autograd(_aux_backward, setup_context=_aux_setup)
+
+
+# ------------------------------------------- the step before: norm -> router
+
+
+@torch.library.custom_op(f"{LIB}::rmsnorm_fwd", mutates_args=())
+def rmsnorm_fwd(hidden: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """Qwen3MoeRMSNorm.forward (TF modeling_qwen3_moe.py:294-299): (x like hidden, rstd [T] f32)."""
+    _require_gpu(hidden, weight)
+    _require_bf16("norm input", hidden)
+    _require_bf16("norm weight", weight)
+    H = hidden.shape[-1]
+    h2 = hidden.reshape(-1, H).contiguous()
+    T = h2.shape[0]
+    x = torch.empty_like(h2)
+    rstd = torch.empty(T, dtype=torch.float32, device=hidden.device)
+    call("moe_rmsnorm_fwd", ptr(h2), ptr(weight.contiguous()), T, H, float(eps), ptr(x), ptr(rstd),
+         _stream(hidden), tag="norm_fwd")
+    return x.view(hidden.shape), rstd
+
+
+@rmsnorm_fwd.register_fake
+def _(hidden, weight, eps):
+    return torch.empty_like(hidden), hidden.new_empty(hidden.numel() // hidden.shape[-1], dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{LIB}::rmsnorm_bwd", mutates_args=())
+def rmsnorm_bwd(dx: Tensor, hidden: Tensor, weight: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
+    """(dhidden, dweight) of rmsnorm_fwd (autograd of TF modeling_qwen3_moe.py:294-299)."""
+    H = hidden.shape[-1]
+    h2 = hidden.reshape(-1, H).contiguous()
+    T = h2.shape[0]
+    g = dx.to(BF16).reshape(-1, H).contiguous()
+    dh = torch.empty_like(h2)
+    dw = torch.empty(H, dtype=BF16, device=hidden.device)
+    ws = _ws(_lib.load().moe_rmsnorm_bwd_workspace_bytes(T, H), hidden.device)
+    call("moe_rmsnorm_bwd", ptr(g), None, ptr(h2), ptr(weight.contiguous()), ptr(rstd), T, H, ptr(dh), ptr(dw),
+         ptr(ws), ws.numel(), _stream(hidden), tag="norm_bwd")
+    return dh.view(hidden.shape), dw
+
+
+@rmsnorm_bwd.register_fake
+def _(dx, hidden, weight, rstd):
+    return torch.empty_like(hidden), torch.empty_like(weight)
+
+
+def _norm_setup(ctx, inputs, output):
+    hidden, weight, _eps = inputs
+    _, rstd = output
+    ctx.save_for_backward(hidden, weight, rstd)
+    ctx.mark_non_differentiable(rstd)
+
+
+def _norm_backward(ctx, dx, _drstd):
+    hidden, weight, rstd = ctx.saved_tensors
+    dh, dw = rmsnorm_bwd(dx, hidden, weight, rstd)
+    return dh, dw, None
+
+
+rmsnorm_fwd.register_autograd(_norm_backward, setup_context=_norm_setup)
+
+
+@torch.library.custom_op(f"{LIB}::router_aux_fwd", mutates_args=())
+def router_aux_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool, token_weight: Tensor | None = None,
+                   logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """router_fwd plus the Switch aux loss from the same softmax and top-k: (logits, scores, indices,
+    aux scalar, stats [E+1]); aux equals aux_loss_fwd(logits, token_weight, E, top_k)."""
+    _require_gpu(x, weight, token_weight)
+    _require_bf16("router input", x)
+    _require_bf16("router weight", weight)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    T, H = x.shape
+    E = weight.shape[0]
+    dev = x.device
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    stats = torch.empty(E + 1, dtype=torch.float32, device=dev)
+    bias = None if logit_bias is None else logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    tw = None if token_weight is None else token_weight.float().contiguous()
+    ws = _ws(_lib.load().moe_router_aux_fwd_workspace_bytes(T, H, E), dev)
+    call("moe_router_aux_fwd", ptr(x), ptr(weight), ptr(bias), ptr(tw), ptr(logits), ptr(scores), ptr(idx), T, H, E,
+         top_k, int(norm_topk_prob), ptr(aux), ptr(stats), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
+    return logits, scores, idx, aux, stats
+
+
+@router_aux_fwd.register_fake
+def _(x, weight, top_k, norm_topk_prob, token_weight=None, logit_bias=None):
+    T, E = x.shape[0], weight.shape[0]
+    return (x.new_empty(T, E, dtype=torch.float32), x.new_empty(T, top_k, dtype=torch.float32),
+            x.new_empty(T, top_k, dtype=torch.int64), x.new_empty((), dtype=torch.float32),
+            x.new_empty(E + 1, dtype=torch.float32))
+
+
+def _router_aux_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
+    x, weight, top_k, norm, token_weight, _bias = inputs
+    logits, _, idx, _, stats = output
+    ctx.save_for_backward(x, weight, logits, idx, token_weight, stats)
+    ctx.norm = norm
+    ctx.mark_non_differentiable(idx, stats)
+
+
+def _router_aux_backward(ctx, d_logits, d_scores, _d_idx, d_aux, _d_stats):
+    x, weight, logits, idx, token_weight, stats = ctx.saved_tensors
+    dl = d_logits
+    if d_aux is not None:
+        dl_aux = aux_loss_bwd(logits, token_weight, stats, d_aux)
+        dl = dl_aux if dl is None else dl.float() + dl_aux
+    dx, dw = router_bwd(x, weight, logits, idx, dl, d_scores, ctx.norm)
+    return dx, dw, None, None, None, None
+
+
+router_aux_fwd.register_autograd(_router_aux_backward, setup_context=_router_aux_setup)
 
 
 # ------------------------------------------------------------------ permute
