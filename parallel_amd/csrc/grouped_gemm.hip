@@ -13,15 +13,21 @@
 // (512x128 when the output is at most 1024 columns wide) on 8 waves (two waves
 // per SIMD, one workgroup per CU); the small router GEMMs use 128x128 on 4
 // waves.  Operands move from HBM to LDS by DMA (buffer_load_dwordx4 ... lds,
-// no register staging) into a 3- or 4-deep ring of 32-deep k-tiles, so two
-// or three k-tiles of loads are in flight while one is multiplied; each wave
-// fires its share of a k-tile's DMA between its MFMA groups.  Each operand
+// no register staging) into a 4- or 5-deep ring of 32-deep k-tiles that fills
+// the 160 KiB of LDS, so three or four k-tiles of loads are in flight while
+// one is multiplied; each wave fires its share of a k-tile's DMA between its
+// MFMA groups.  At the roughly 256 rows per expert of a training step the
+// expert GEMMs sit near the ridge of the roofline (about 256 flop per weight
+// byte), and the weights stream from HBM only as fast as the bytes in flight
+// per CU allow, so the ring takes all of the LDS: the epilogue stages its
+// output through the ring stage it has just multiplied.  Each operand
 // keeps its HBM layout in LDS (XOR swizzled): K-contiguous fragments are
 // ds_read_b128, M/N-contiguous ones (weights in the input gradient, both
 // operands of the weight gradient) are ds_read_b64_tr_b16 transpose reads.
 // Buffer loads read zero past the resource size, so ragged rows and the K
 // tail need no branches.  Row sub-tiles that lie wholly outside the valid
-// rows skip their MFMAs (the last M tile of an expert is usually short).
+// rows skip their MFMAs (an expert's rows are split evenly over its m-tiles,
+// so most m-tiles are partly filled).
 //
 // Tiles are mapped to groups on the device from the `offs` cumsum (no host
 // sync).  The logical tile order is group-major, then n-tile, then m-tile, so
@@ -103,14 +109,14 @@ struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int kThreads = 64 * WM * WN;
 };
-// Expert GEMMs and weight gradients: 128 KiB ring + 32 KiB staging, 8 waves.
-using BigTile = TileCfg<256, 256, 32, 2, 4, 4>;
+// Expert GEMMs and weight gradients: 160 KiB ring, 8 waves.
+using BigTile = TileCfg<256, 256, 32, 2, 4, 5>;
 // Expert GEMMs with narrow outputs: 512-row tiles, so that an expert of up to
 // 512 rows is one m-tile and its weights stream through LDS once per n-tile;
-// 120 KiB ring + 32 KiB staging, 8 waves.
-using TallTile = TileCfg<512, 128, 32, 4, 2, 3>;
-// Router GEMMs (N = E = 128): 64 KiB ring + 16 KiB staging, 4 waves.
-using SmallTile = TileCfg<128, 128, 32, 2, 2, 4>;
+// 160 KiB ring, 8 waves.
+using TallTile = TileCfg<512, 128, 32, 4, 2, 4>;
+// Router GEMMs (N = E = 128): 80 KiB ring, 4 waves (two workgroups per CU).
+using SmallTile = TileCfg<128, 128, 32, 2, 2, 5>;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
@@ -251,13 +257,13 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
   static_assert(NI_A % NWAVES == 0 && NI_B % NWAVES == 0, "DMA instructions of each operand split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
-  static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+  static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
+  static_assert(NWAVES * SLOT <= STAGE_BYTES, "the epilogue stages every wave's pass in one ring stage");
   static_assert(WAIT + NST < 64, "vmcnt range");
   static_assert(A_KC || BM >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
   static_assert(B_KC || BN >= 128, "transpose-read swizzle needs >= 16 chunks per k-row");
 
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char staging[NWAVES * SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -280,8 +286,8 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
 
   // Lane l of a descriptor chunk describes block tile 64 * chunk + l:
   // group, first output row (absolute for MG, within the group for KG),
-  // first output column, reduction rows [rb, re) (KG) or valid rows end (MG),
-  // split-K index.
+  // first output column, reduction rows [rb, re) (KG) or the tile's valid
+  // rows end (MG), split-K index.
   struct Desc {
     int g, m0, n0, rb, re, split;
   };
@@ -326,7 +332,15 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
           const int local = L - t0;
           const int mt_g = (cn + BM - 1) / BM;
           const int nt = local / mt_g, mt = local - (local / mt_g) * mt_g;
-          d = Desc{tg, r0 + mt * BM, nt * BN, r0, r0 + cn, 0};
+          // The group's rows split evenly over its m-tiles (whole 32-row
+          // sub-tiles): the m-tiles of one weight tile then run at the same
+          // pace on neighbouring CUs and read each weight k-slice once from
+          // HBM between them, where a full tile plus a short one would drift
+          // apart and read it twice.  Every m-tile holds rows, since
+          // (mt_g - 1) * rpt <= (mt_g - 1) * BM < cn.
+          const int rpt = min(BM, ((cn + mt_g - 1) / mt_g + 31) & ~31);
+          const int m0 = r0 + mt * rpt;
+          d = Desc{tg, m0, nt * BN, r0, min(m0 + rpt, r0 + cn), 0};
         }
       } else {
         const int mtiles = (p.M + BM - 1) / BM;
@@ -623,7 +637,14 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // ------------------------------------------------------ epilogue
   // Lane owns output row  m0 + sub_row(i) + l32  and columns
   // wcol0 + j*32 + 8*q + 4*khalf + {0..3} holding acc[i][j][4q..4q+3].
-  char* slot = staging + wave * SLOT;  // this wave's staging slot (no other wave touches it)
+  // This wave's staging slot (no other wave touches it) in the ring stage
+  // that the compute cursor has just finished: no DMA targets that stage
+  // until the next k-step's barrier, and a barrier before the epilogue
+  // retires every wave's fragment reads of it.  Tiles written out before the
+  // stream starts (empty weight-gradient groups) use the last stage, which
+  // the prologue DMA into stages 0 .. STAGES-2 leaves alone and the first
+  // k-step fills only after its barrier.
+  char* slot = ring + (STAGES - 1) * STAGE_BYTES + wave * SLOT;
   auto swap_halves = [](uint4 v) { return make_uint4(v.z, v.w, v.x, v.y); };
   auto to_f32x8 = [](uint4 v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -844,6 +865,8 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
       cstage = cstage + 1 == STAGES ? 0 : cstage + 1;
       if (++ck == ct.nk) {
+        slot = ring + (cstage == 0 ? STAGES - 1 : cstage - 1) * STAGE_BYTES + wave * SLOT;
+        barrier();
         epilogue(ct);
         relax = STAGES - 1;
         if (!compute_seek(cj + 1)) break;

@@ -203,6 +203,7 @@ GEMM_CASES = [
     ("c2like", [256, 0, 300, 1, 128, 255, 513], 1536, 2048),
     ("ragged", [7, 0, 0, 130, 64, 1], 200, 72),
     ("single", [1000], 128, 256),
+    ("split", [770, 257, 33], 1280, 64),  # m-tiles of 224/224/224/98 and 160/97 rows
 ]
 
 
