@@ -16,13 +16,19 @@ constexpr int kMaxPerLane = 16;  // E <= 1024
 constexpr int kMaxTopK = 16;
 constexpr int kRouterWaves = 4;  // waves per block
 
+// The kernels are instantiated per NPL (experts per lane, E <= 64 NPL, a power
+// of two) and KT (top-k; 0 = any k up to kMaxTopK), so that the per-lane loops
+// have fixed trip counts.  Items of lanes past E read as -inf and are never
+// selected; the arithmetic is that of any NPL large enough for E.
+
 // Loads one token's logits; absent experts read as -inf.
-__device__ __forceinline__ void load_row(const float* row, int E, float (&v)[kMaxPerLane], int npl) {
+template <int NPL>
+__device__ __forceinline__ void load_row(const float* row, int E, float (&v)[NPL]) {
   const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
-    v[j] = (j < npl && e < E) ? row[e] : -INFINITY;
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + j * kWave;
+    v[j] = e < E ? row[e] : -INFINITY;
   }
 }
 
@@ -30,164 +36,180 @@ struct SoftmaxStats {
   float max, sum;
 };
 
-__device__ __forceinline__ SoftmaxStats softmax_stats(const float (&v)[kMaxPerLane], int npl) {
+template <int NPL>
+__device__ __forceinline__ SoftmaxStats softmax_stats(const float (&v)[NPL]) {
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j)
-    if (j < npl) m = fmaxf(m, v[j]);
+  for (int j = 0; j < NPL; ++j) m = fmaxf(m, v[j]);
   m = wave_max(m);
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j)
-    if (j < npl && v[j] != -INFINITY) s += expf(v[j] - m);
+  for (int j = 0; j < NPL; ++j)
+    if (v[j] != -INFINITY) s += expf(v[j] - m);
   s = wave_sum(s);
   return {m, s};
 }
 
 // k-way selection: sel_idx/sel_logit are wave-uniform after the call.
-__device__ __forceinline__ void select_topk(const float (&v)[kMaxPerLane], int npl, int E, int k,
-                                            int (&sel_idx)[kMaxTopK], float (&sel_logit)[kMaxTopK]) {
+template <int NPL, int KM>
+__device__ __forceinline__ void select_topk(const float (&v)[NPL], int E, int k, int (&sel_idx)[KM],
+                                            float (&sel_logit)[KM]) {
   const int lane = threadIdx.x & (kWave - 1);
   unsigned taken = 0;  // bit j: item j of this lane already selected
-  for (int r = 0; r < k; ++r) {
-    float best = -INFINITY;
-    int bidx = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      int e = lane + j * kWave;
-      // Items are visited in increasing e, so ">" keeps the lower index on
-      // ties; the first live item is always taken (covers -inf logits).
-      if (j < npl && e < E && !(taken & (1u << j)) && (v[j] > best || bidx == 0x7fffffff)) {
-        best = v[j];
-        bidx = e;
+  for (int r = 0; r < KM; ++r) {
+    if (r < k) {
+      float best = -INFINITY;
+      int bidx = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const int e = lane + j * kWave;
+        // Items are visited in increasing e, so ">" keeps the lower index on
+        // ties; the first live item is always taken (covers -inf logits).
+        if (e < E && !(taken & (1u << j)) && (v[j] > best || bidx == 0x7fffffff)) {
+          best = v[j];
+          bidx = e;
+        }
       }
+      wave_argmax(best, bidx);
+      sel_idx[r] = bidx;
+      sel_logit[r] = best;
+      if (bidx != 0x7fffffff && (bidx & (kWave - 1)) == lane) taken |= 1u << (bidx / kWave);
     }
-    wave_argmax(best, bidx);
-    sel_idx[r] = bidx;
-    sel_logit[r] = best;
-    if (bidx != 0x7fffffff && (bidx & (kWave - 1)) == lane) taken |= 1u << (bidx / kWave);
   }
 }
 
-__global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_fwd_kernel(const float* __restrict__ logits,
-                                                                                float* __restrict__ scores,
-                                                                                int64_t* __restrict__ indices, int T,
-                                                                                int E, int k, int norm) {
+// Top-k probabilities of the selection, then the scores (renormalised with
+// `norm`) and indices written by lanes 0 .. k-1.
+template <int KM>
+__device__ __forceinline__ void write_topk(const SoftmaxStats& st, const int (&sel)[KM], const float (&sl)[KM], int k,
+                                           int norm, float* __restrict__ scores, int64_t* __restrict__ indices,
+                                           int64_t t) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int npl = (E + kWave - 1) / kWave;
-  float v[kMaxPerLane];
-  load_row(logits + static_cast<int64_t>(t) * E, E, v, npl);
-  SoftmaxStats st = softmax_stats(v, npl);
-  int sel[kMaxTopK];
-  float sl[kMaxTopK];
-  select_topk(v, npl, E, k, sel, sl);
-  float pv[kMaxTopK];
+  float pv[KM];
   float tot = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
+  for (int r = 0; r < KM; ++r) {
     if (r < k) {
       pv[r] = expf(sl[r] - st.max) / st.sum;
       tot += pv[r];
     }
   }
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
+  for (int r = 0; r < KM; ++r) {
     if (r < k && lane == r) {
-      scores[static_cast<int64_t>(t) * k + r] = norm ? pv[r] / tot : pv[r];
-      indices[static_cast<int64_t>(t) * k + r] = sel[r];
+      scores[t * k + r] = norm ? pv[r] / tot : pv[r];
+      indices[t * k + r] = sel[r];
     }
   }
+}
+
+template <int NPL, int KT>
+__global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_fwd_kernel(const float* __restrict__ logits,
+                                                                                float* __restrict__ scores,
+                                                                                int64_t* __restrict__ indices, int T,
+                                                                                int E, int k_rt, int norm) {
+  constexpr int KM = KT ? KT : kMaxTopK;
+  const int k = KT ? KT : k_rt;
+  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[NPL];
+  load_row(logits + static_cast<int64_t>(t) * E, E, v);
+  const SoftmaxStats st = softmax_stats(v);
+  int sel[KM];
+  float sl[KM];
+  select_topk(v, E, k, sel, sl);
+  write_topk(st, sel, sl, k, norm, scores, indices, t);
 }
 
 // logits[t] = sum_s partials[s][t] (+ bias), then the top-k softmax of that row.
 // With aux_ws, also the aux-loss partials of the block's 4 tokens from the
 // same softmax and selection (the layout and arithmetic of aux_partial_kernel).
+template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kernel(
     const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
-    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k, int norm,
+    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k_rt, int norm,
     const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
-  __shared__ float part[kRouterWaves][2 * 1024 + 1];
+  constexpr int KM = KT ? KT : kMaxTopK;
+  const int k = KT ? KT : k_rt;
+  __shared__ float part[kRouterWaves][2 * kWave * NPL + 1];  // E <= 64 NPL
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * kRouterWaves + wave;
   if (t >= T && !aux_ws) return;
-  const int npl = (E + kWave - 1) / kWave;
   const int64_t plane = static_cast<int64_t>(T) * E;
-  float v[kMaxPerLane];
-  float P[kMaxPerLane], C[kMaxPerLane];
+  float P[NPL], C[NPL];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) P[j] = C[j] = 0.0f;
+  for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
   float W = 0.0f;
   if (t < T) {
+    float v[NPL];
+    // All of the lane's split loads are issued before any add; the adds go
+    // in split order.
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
-    v[j] = -INFINITY;
-    if (j < npl && e < E) {
-      const float* src = partials + static_cast<int64_t>(t) * E + e;
-      // Loads in batches of 8 (independent), added in split order.
-      float acc = 0.0f;
-      int sp = 0;
-      for (; sp + 8 <= splits; sp += 8) {
-        float q[8];
+    for (int j = 0; j < NPL; ++j) v[j] = 0.0f;
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+      float q[8][NPL];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) q[u] = src[(sp + u) * plane];
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc += q[u];
-      }
-      for (; sp < splits; ++sp) acc += src[sp * plane];
-      if (bias) acc += bias[e];
-      v[j] = acc;
-      logits[static_cast<int64_t>(t) * E + e] = acc;
+        for (int j = 0; j < NPL; ++j) {
+          const int e = lane + j * kWave;
+          q[u][j] = e < E ? partials[(sp + u) * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
+        }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) v[j] += q[u][j];
     }
-  }
-  SoftmaxStats st = softmax_stats(v, npl);
-  int sel[kMaxTopK];
-  float sl[kMaxTopK];
-  select_topk(v, npl, E, k, sel, sl);
-  float pv[kMaxTopK];
-  float tot = 0.0f;
+    for (; sp < splits; ++sp) {
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
-    if (r < k) {
-      pv[r] = expf(sl[r] - st.max) / st.sum;
-      tot += pv[r];
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
-    if (r < k && lane == r) {
-      scores[static_cast<int64_t>(t) * k + r] = norm ? pv[r] / tot : pv[r];
-      indices[static_cast<int64_t>(t) * k + r] = sel[r];
-    }
-  }
-  if (aux_ws) {
-    const float w = token_weight ? token_weight[t] : 1.0f;
-    W = w;
-    const float inv_sum = 1.0f / st.sum;
-#pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      int e = lane + j * kWave;
-      if (j < npl && e < E) {
-        P[j] = w * (expf(v[j] - st.max) * inv_sum);
-        float cnt = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kMaxTopK; ++r)
-          if (r < k && sel[r] == e) cnt += 1.0f;
-        C[j] = w * cnt;
+      for (int j = 0; j < NPL; ++j) {
+        const int e = lane + j * kWave;
+        v[j] += e < E ? partials[sp * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
       }
     }
-  }
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int e = lane + j * kWave;
+      if (e < E) {
+        if (bias) v[j] += bias[e];
+        logits[static_cast<int64_t>(t) * E + e] = v[j];
+      } else {
+        v[j] = -INFINITY;
+      }
+    }
+    const SoftmaxStats st = softmax_stats(v);
+    int sel[KM];
+    float sl[KM];
+    select_topk(v, E, k, sel, sl);
+    write_topk(st, sel, sl, k, norm, scores, indices, t);
+    if (aux_ws) {
+      const float w = token_weight ? token_weight[t] : 1.0f;
+      W = w;
+      const float inv_sum = 1.0f / st.sum;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const int e = lane + j * kWave;
+        if (e < E) {
+          P[j] = w * (expf(v[j] - st.max) * inv_sum);
+          float cnt = 0.0f;
+#pragma unroll
+          for (int r = 0; r < KM; ++r)
+            if (r < k && sel[r] == e) cnt += 1.0f;
+          C[j] = w * cnt;
+        }
+      }
+    }
   }  // t < T
   if (aux_ws) {
     // The block's 4 tokens, added in wave order (aux_partial_kernel's sums
     // start from zero, so each wave's term is 0 + term).
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      int e = lane + j * kWave;
-      if (j < npl && e < E) {
+    for (int j = 0; j < NPL; ++j) {
+      const int e = lane + j * kWave;
+      if (e < E) {
         part[wave][e] = 0.0f + P[j];
         part[wave][E + e] = 0.0f + C[j];
       }
@@ -221,24 +243,26 @@ __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, 
 }
 
 // d_logits = p * (dp - <dp, p>), dp scattered from the (renormalised) top-k.
+template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ indices, const float* __restrict__ d_scores, int T,
-    int E, int k, int norm, float* __restrict__ d_logits, int accumulate, bf16_t* __restrict__ d_logits_bf16) {
+    int E, int k_rt, int norm, float* __restrict__ d_logits, int accumulate, bf16_t* __restrict__ d_logits_bf16) {
+  constexpr int KM = KT ? KT : kMaxTopK;
+  const int k = KT ? KT : k_rt;
   const int lane = threadIdx.x & (kWave - 1);
   const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int npl = (E + kWave - 1) / kWave;
-  float v[kMaxPerLane];
+  float v[NPL];
   const float* row = logits + static_cast<int64_t>(t) * E;
-  load_row(row, E, v, npl);
-  SoftmaxStats st = softmax_stats(v, npl);
+  load_row(row, E, v);
+  const SoftmaxStats st = softmax_stats(v);
   const float inv_sum = 1.0f / st.sum;
 
-  int idx[kMaxTopK];
-  float pv[kMaxTopK], ds[kMaxTopK];
+  int idx[KM];
+  float pv[KM], ds[KM];
   float tot = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
+  for (int r = 0; r < KM; ++r) {
     if (r < k) {
       int64_t id = indices[static_cast<int64_t>(t) * k + r];
       bool ok = id >= 0 && id < E;
@@ -249,33 +273,33 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     }
   }
   // Renormalisation backward: s_r = v_r / V  ->  dv_r = (ds_r - sum_i ds_i s_i) / V.
-  float dv[kMaxTopK];
+  float dv[KM];
   if (norm) {
     float dot = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r)
+    for (int r = 0; r < KM; ++r)
       if (r < k) dot += ds[r] * (pv[r] / tot);
 #pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r)
+    for (int r = 0; r < KM; ++r)
       if (r < k) dv[r] = (ds[r] - dot) / tot;
   } else {
 #pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r)
+    for (int r = 0; r < KM; ++r)
       if (r < k) dv[r] = ds[r];
   }
   float c = 0.0f;  // <dp, p> = sum_r dv_r p_{idx_r}
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r)
+  for (int r = 0; r < KM; ++r)
     if (r < k) c += dv[r] * pv[r];
 
   float* drow = d_logits + static_cast<int64_t>(t) * E;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
-    if (j < npl && e < E) {
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + j * kWave;
+    if (e < E) {
       float dp = 0.0f;
 #pragma unroll
-      for (int r = 0; r < kMaxTopK; ++r)
+      for (int r = 0; r < KM; ++r)
         if (r < k && idx[r] == e) dp += dv[r];
       float p = expf(v[j] - st.max) * inv_sum;
       float g = p * (dp - c);
@@ -298,46 +322,48 @@ int aux_blocks(int64_t T) {
 }
 
 // Per block partials: ws[b] = (P_0..P_{E-1}, c_0..c_{E-1}, W), fixed-order sums.
+template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void aux_partial_kernel(const float* __restrict__ logits,
                                                                             const float* __restrict__ token_weight,
-                                                                            int T, int E, int k,
+                                                                            int T, int E, int k_rt,
                                                                             float* __restrict__ ws) {
-  __shared__ float part[kRouterWaves][2 * 1024 + 1];
+  constexpr int KM = KT ? KT : kMaxTopK;
+  const int k = KT ? KT : k_rt;
+  __shared__ float part[kRouterWaves][2 * kWave * NPL + 1];  // E <= 64 NPL
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
-  const int npl = (E + kWave - 1) / kWave;
-  float P[kMaxPerLane], C[kMaxPerLane];
+  float P[NPL], C[NPL];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) P[j] = C[j] = 0.0f;
+  for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
   float W = 0.0f;
   const int waves_total = gridDim.x * kRouterWaves;
   for (int t = blockIdx.x * kRouterWaves + wave; t < T; t += waves_total) {
-    float v[kMaxPerLane];
-    load_row(logits + static_cast<int64_t>(t) * E, E, v, npl);
-    SoftmaxStats st = softmax_stats(v, npl);
-    int sel[kMaxTopK];
-    float sl[kMaxTopK];
-    select_topk(v, npl, E, k, sel, sl);
+    float v[NPL];
+    load_row(logits + static_cast<int64_t>(t) * E, E, v);
+    const SoftmaxStats st = softmax_stats(v);
+    int sel[KM];
+    float sl[KM];
+    select_topk(v, E, k, sel, sl);
     const float w = token_weight ? token_weight[t] : 1.0f;
     W += w;
     const float inv_sum = 1.0f / st.sum;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      int e = lane + j * kWave;
-      if (j < npl && e < E) {
+    for (int j = 0; j < NPL; ++j) {
+      const int e = lane + j * kWave;
+      if (e < E) {
         P[j] += w * (expf(v[j] - st.max) * inv_sum);
         float cnt = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kMaxTopK; ++r)
+        for (int r = 0; r < KM; ++r)
           if (r < k && sel[r] == e) cnt += 1.0f;
         C[j] += w * cnt;
       }
     }
   }
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
-    if (j < npl && e < E) {
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + j * kWave;
+    if (e < E) {
       part[wave][e] = P[j];
       part[wave][E + e] = C[j];
     }
@@ -408,6 +434,7 @@ __global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restr
   if (tid == 0) aux[0] = static_cast<float>(E) * terms[0];
 }
 
+template <int NPL>
 __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const float* __restrict__ logits,
                                                                         const float* __restrict__ token_weight,
                                                                         const float* __restrict__ stats,
@@ -416,22 +443,21 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
   const int lane = threadIdx.x & (kWave - 1);
   const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int npl = (E + kWave - 1) / kWave;
-  float v[kMaxPerLane];
-  load_row(logits + static_cast<int64_t>(t) * E, E, v, npl);
-  SoftmaxStats st = softmax_stats(v, npl);
+  float v[NPL];
+  load_row(logits + static_cast<int64_t>(t) * E, E, v);
+  const SoftmaxStats st = softmax_stats(v);
   const float inv_sum = 1.0f / st.sum;
   const float W = stats[E];
   const float w = token_weight ? token_weight[t] : 1.0f;
   const float scale = d_aux[0] * static_cast<float>(E) * w / (W * W);
-  float p[kMaxPerLane], g[kMaxPerLane];
+  float p[NPL], g[NPL];
   float dot = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + j * kWave;
     p[j] = 0.0f;
     g[j] = 0.0f;
-    if (j < npl && e < E) {
+    if (e < E) {
       p[j] = expf(v[j] - st.max) * inv_sum;
       g[j] = scale * stats[e];
       dot += p[j] * g[j];
@@ -440,9 +466,9 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
   dot = wave_sum(dot);
   float* drow = d_logits + static_cast<int64_t>(t) * E;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    int e = lane + j * kWave;
-    if (j < npl && e < E) {
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + j * kWave;
+    if (e < E) {
       float d = p[j] * (g[j] - dot);
       drow[e] = accumulate ? drow[e] + d : d;
     }
@@ -454,6 +480,31 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
 using namespace moe;
 
 namespace {
+// Instantiation for E experts (experts per lane rounded up to a power of two)
+// and top-k k (the specialised k, or the generic 0).
+template <class F>
+void with_npl(int64_t E, F&& f) {
+  const int64_t n = (E + kWave - 1) / kWave;
+  if (n <= 1) f(std::integral_constant<int, 1>{});
+  else if (n <= 2) f(std::integral_constant<int, 2>{});
+  else if (n <= 4) f(std::integral_constant<int, 4>{});
+  else if (n <= 8) f(std::integral_constant<int, 8>{});
+  else f(std::integral_constant<int, 16>{});
+}
+template <class F>
+void with_npl_k(int64_t E, int64_t k, F&& f) {
+  with_npl(E, [&](auto N) {
+    switch (k) {
+      case 1: f(N, std::integral_constant<int, 1>{}); break;
+      case 2: f(N, std::integral_constant<int, 2>{}); break;
+      case 4: f(N, std::integral_constant<int, 4>{}); break;
+      case 6: f(N, std::integral_constant<int, 6>{}); break;
+      case 8: f(N, std::integral_constant<int, 8>{}); break;
+      default: f(N, std::integral_constant<int, 0>{}); break;
+    }
+  });
+}
+
 int check_router(int64_t T, int64_t E, int64_t k) {
   MOE_REQUIRE(T >= 0 && T < (1ll << 31), MOE_ERR_INVALID, "router: bad token count %lld", (long long)T);
   MOE_REQUIRE(E >= 1 && E <= kMaxPerLane * kWave, MOE_ERR_UNSUPPORTED, "router: E=%lld outside [1,%d]", (long long)E,
@@ -471,9 +522,11 @@ extern "C" int moe_router_topk_fwd(const float* logits, float* scores, int64_t* 
   MOE_REQUIRE(logits && scores && indices, MOE_ERR_INVALID, "router topk: null pointer");
   if (T == 0) return MOE_OK;
   int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  hipLaunchKernelGGL(router_topk_fwd_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, as_stream(stream), logits,
-                     scores, indices, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k),
-                     norm_topk_prob ? 1 : 0);
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, scores, indices, static_cast<int>(T),
+                       static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0);
+  });
   return launch_status("moe_router_topk_fwd");
 }
 
@@ -485,9 +538,12 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
   MOE_REQUIRE(logits && indices && d_scores && d_logits, MOE_ERR_INVALID, "router topk bwd: null pointer");
   if (T == 0) return MOE_OK;
   int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  hipLaunchKernelGGL(router_topk_bwd_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, as_stream(stream), logits,
-                     indices, d_scores, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k),
-                     norm_topk_prob ? 1 : 0, d_logits, accumulate ? 1 : 0, static_cast<bf16_t*>(d_logits_bf16));
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
+                       d_logits, accumulate ? 1 : 0, static_cast<bf16_t*>(d_logits_bf16));
+  });
   return launch_status("moe_router_topk_bwd");
 }
 
@@ -506,8 +562,11 @@ extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, 
               "aux loss: workspace %zu < %zu bytes", workspace_bytes, moe_aux_loss_workspace_bytes(T, E));
   const int nblk = aux_blocks(T);
   float* ws = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(aux_partial_kernel, dim3(nblk), dim3(kRouterWaves * kWave), 0, as_stream(stream), logits,
-                     token_weight, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), ws);
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((aux_partial_kernel<decltype(N)::value, decltype(K)::value>), dim3(nblk),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, token_weight, static_cast<int>(T),
+                       static_cast<int>(E), static_cast<int>(k), ws);
+  });
   rc = launch_status("moe_aux_loss_fwd(partial)");
   if (rc) return rc;
   const int n = static_cast<int>(2 * E + 1);
@@ -528,9 +587,11 @@ extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, 
   MOE_REQUIRE(logits && stats && d_aux && d_logits, MOE_ERR_INVALID, "aux loss bwd: null pointer");
   if (T == 0) return MOE_OK;
   int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  hipLaunchKernelGGL(aux_bwd_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, as_stream(stream), logits,
-                     token_weight, stats, d_aux, static_cast<int>(T), static_cast<int>(E), d_logits,
-                     accumulate ? 1 : 0);
+  with_npl(E, [&](auto N) {
+    hipLaunchKernelGGL((aux_bwd_kernel<decltype(N)::value>), dim3(blocks), dim3(kRouterWaves * kWave), 0,
+                       as_stream(stream), logits, token_weight, stats, d_aux, static_cast<int>(T),
+                       static_cast<int>(E), d_logits, accumulate ? 1 : 0);
+  });
   return launch_status("moe_aux_loss_bwd");
 }
 
@@ -577,9 +638,12 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
                               static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
   if (rc) return rc;
   int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  hipLaunchKernelGGL(router_reduce_topk_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits,
-                     logit_bias, logits, scores, indices, static_cast<int>(T), static_cast<int>(E),
-                     static_cast<int>(k), norm_topk_prob ? 1 : 0, nullptr, nullptr);
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
+                       nullptr, nullptr);
+  });
   return launch_status("moe_router_fwd(reduce+topk)");
 }
 
@@ -614,9 +678,12 @@ extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* lo
                               static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
   if (rc) return rc;
   const int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  hipLaunchKernelGGL(router_reduce_topk_kernel, dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits,
-                     logit_bias, logits, scores, indices, static_cast<int>(T), static_cast<int>(E),
-                     static_cast<int>(k), norm_topk_prob ? 1 : 0, token_weight, aux_ws);
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
+                       token_weight, aux_ws);
+  });
   rc = launch_status("moe_router_aux_fwd(reduce+topk+aux partials)");
   if (rc) return rc;
   const int n = static_cast<int>(2 * E + 1);
