@@ -106,7 +106,7 @@ _GEMM_ORDER = {
     (0, True, 2): ["up_fwd"],
     (0, True, 0): ["down_fwd"],
     (0, False, 0): ["down_dgrad", "up_dgrad"],  # backward runs the down projection first
-    (1, False, 4): ["down_wgrad", "up_wgrad"],
+    (1, False, 4): ["up_wgrad", "down_wgrad"],  # ... and the weight gradients last, up first
 }
 
 

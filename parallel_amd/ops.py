@@ -477,18 +477,22 @@ def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down
     d_pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
     call("moe_grouped_gemm_dgrad_swiglu_bwd", ptr(dy), ptr(down_proj), ptr(pre), ptr(offsets), E, S, H, I,
          ptr(d_pre), s, tag="down_dgrad")
-    d_down = torch.empty_like(down_proj)
-    call("moe_grouped_gemm_wgrad", ptr(dy), ptr(act), ptr(offsets), E, S, H, I, ptr(d_down), 0, 0, s,
-         tag="down_wgrad")
+    # Each consumer runs right after its producer while the tensor is still in
+    # the 256 MB last-level cache: the input-gradient GEMM reads d_pre, the
+    # permute backward reads d_xp; the weight gradients (1.2 GB of writes
+    # that would evict both) come last.
     d_xp = torch.empty(S, H, dtype=BF16, device=dev)
     call("moe_grouped_gemm_dgrad", ptr(d_pre), ptr(gate_up_proj), ptr(offsets), E, S, 2 * I, H, ptr(d_xp), s,
          tag="up_dgrad")
-    d_gu = torch.empty_like(gate_up_proj)
-    call("moe_grouped_gemm_wgrad", ptr(d_pre), ptr(xp), ptr(offsets), E, S, 2 * I, H, ptr(d_gu), 0, 0, s,
-         tag="up_wgrad")
     d_hidden = torch.empty(T, H, dtype=BF16, device=dev)
     call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, None, ptr(d_hidden), s,
          tag="permute_bwd")
+    d_gu = torch.empty_like(gate_up_proj)
+    call("moe_grouped_gemm_wgrad", ptr(d_pre), ptr(xp), ptr(offsets), E, S, 2 * I, H, ptr(d_gu), 0, 0, s,
+         tag="up_wgrad")
+    d_down = torch.empty_like(down_proj)
+    call("moe_grouped_gemm_wgrad", ptr(dy), ptr(act), ptr(offsets), E, S, H, I, ptr(d_down), 0, 0, s,
+         tag="down_wgrad")
     return d_hidden, d_w, d_gu, d_down
 
 

@@ -123,18 +123,18 @@ def test_bench_tags_kernel_dispatches_by_entry_point():
     import bench
 
     g = "void moe::grouped_gemm_kernel<{}, {}, {}, moe::TileCfg<{}> >(moe::GemmParams)"
-    big, tall, small = "256, 256, 32, 2, 4, 4", "512, 128, 32, 4, 2, 3", "128, 128, 32, 2, 2, 4"
+    big, tall, small = "256, 256, 32, 2, 4, 5", "512, 128, 32, 4, 2, 4", "128, 128, 32, 2, 2, 5"
     names = [
-        g.format(0, "true", 1, small), "moe::router_reduce_topk_kernel(float const*)",
+        g.format(0, "true", 1, small), "void moe::router_reduce_topk_kernel<2, 8>(float const*)",
         g.format(0, "true", 2, big), g.format(0, "true", 0, big), "void moe::combine_fwd_kernel<8>(unsigned short const*)",
         "void moe::combine_bwd_kernel<8>(unsigned short const*)",
-        g.format(0, "false", 0, tall), "moe::swiglu_bwd_kernel(unsigned short*)", g.format(1, "false", 4, big),
-        g.format(0, "false", 0, big), g.format(1, "false", 4, big),
-        "void moe::permute_bwd_kernel<8>(unsigned short const*)",
+        g.format(0, "false", 0, tall), "moe::swiglu_bwd_kernel(unsigned short*)", g.format(0, "false", 0, big),
+        "void moe::permute_bwd_kernel<8>(unsigned short const*)", g.format(1, "false", 4, big),
+        g.format(1, "false", 4, big),
         g.format(1, "false", 4, small), g.format(0, "false", 0, small),
     ]
     assert bench.tag_dispatches(names) == [
         "router_fwd", "router_fwd", "up_fwd", "down_fwd", "combine_fwd", "combine_bwd",
-        "down_dgrad", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad", "permute_bwd",
+        "down_dgrad", "down_dgrad", "up_dgrad", "permute_bwd", "up_wgrad", "down_wgrad",
         "router_gemm_bwd", "router_gemm_bwd",
     ]
