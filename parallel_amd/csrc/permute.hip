@@ -4,9 +4,10 @@
 // in three small launches plus one bandwidth-bound row gather:
 //   1. count:   each block histograms a CHUNK of slots in LDS (integer
 //               atomics, so counts are exact and order-free);
-//   2. scan:    one block turns the [blocks x buckets] histogram into the
-//               first sorted position of every (block, bucket) pair, plus the
-//               per-bucket counts and inclusive offsets;
+//   2. scan:    one block turns the [blocks x buckets] histogram into
+//               per-bucket prefixes over the blocks, plus the per-bucket
+//               counts and inclusive offsets (a block's first position in a
+//               bucket is its prefix plus the bucket's start);
 //   3. scatter: each block re-walks its chunk 256 slots at a time; a wave
 //               finds equal keys with one ballot per key bit, ranks a slot by
 //               the popcount of equal-key lanes below it, and waves are
@@ -24,6 +25,7 @@ namespace moe {
 
 constexpr int kChunk = 2048;       // slots per block in count/scatter
 constexpr int kPermThreads = 256;  // 4 waves
+constexpr int kPerThread = kChunk / kPermThreads;
 constexpr int kMaxBuckets = 1024;  // real buckets; +1 for the sentinel bucket
 
 __device__ __forceinline__ int bucket_of(int64_t id, int64_t divisor, int nb) {
@@ -40,12 +42,24 @@ __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(const int64
   __syncthreads();
   const int begin = blockIdx.x * kChunk;
   const int end = min(begin + kChunk, S);
-  for (int s = begin + threadIdx.x; s < end; s += kPermThreads) atomicAdd(&h[bucket_of(ids[s], divisor, nb)], 1);
+  // All of the thread's ids in flight at once, then the LDS atomics.
+  int64_t id[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r) {
+    const int s = begin + r * kPermThreads + threadIdx.x;
+    id[r] = s < end ? ids[s] : -1;
+  }
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r)
+    if (begin + r * kPermThreads + static_cast<int>(threadIdx.x) < end) atomicAdd(&h[bucket_of(id[r], divisor, nb)], 1);
   __syncthreads();
   for (int i = threadIdx.x; i < nb1; i += kPermThreads) hist[static_cast<int64_t>(blockIdx.x) * nb1 + i] = h[i];
 }
 
-// hist[b][e] (counts) -> base[b][e] (first sorted position), in place.
+// hist[b][e] (counts) -> the exclusive prefix over blocks b of bucket e, in
+// place; counts[e] and inclusive offsets[e] for the real buckets.  Block b's
+// first sorted position for bucket e is hist[b][e] + start(e), with start(e) =
+// offsets[e] - counts[e] (and offsets[nb - 1] for the sentinel bucket).
 __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict__ hist, int nblk, int nb,
                                                             int32_t* __restrict__ counts,
                                                             int32_t* __restrict__ offsets) {
@@ -54,56 +68,60 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
   const int nb1 = nb + 1;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wave = tid >> 6;
-  // Column prefix over blocks (per bucket), exclusive.
+  // Column prefix over blocks (per bucket), exclusive; 16 rows' loads in
+  // flight at a time.
+  constexpr int kRows = 16;
   for (int e = tid; e < nb1; e += blockDim.x) {
     int run = 0;
-    for (int b = 0; b < nblk; ++b) {
-      int64_t o = static_cast<int64_t>(b) * nb1 + e;
-      int c = hist[o];
-      hist[o] = run;
-      run += c;
+    for (int b0 = 0; b0 < nblk; b0 += kRows) {
+      int c[kRows];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) c[r] = b0 + r < nblk ? hist[static_cast<int64_t>(b0 + r) * nb1 + e] : 0;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        if (b0 + r < nblk) hist[static_cast<int64_t>(b0 + r) * nb1 + e] = run;
+        run += c[r];
+      }
     }
     tot[e] = run;
   }
   __syncthreads();
-  // Exclusive scan over buckets (nb1 <= 1025 entries; two passes of 1024).
-  __shared__ int start[kMaxBuckets + 1];
-  int carry = 0;
-  for (int base = 0; base < nb1; base += 1024) {
-    int e = base + tid;
-    int v = e < nb1 ? tot[e] : 0;
-    int incl = wave_inclusive_scan(v);
-    if (lane == kWave - 1) wsum[wave] = incl;
-    __syncthreads();
-    int wprefix = 0;
-    for (int w = 0; w < wave; ++w) wprefix += wsum[w];
-    if (e < nb1) start[e] = carry + wprefix + incl - v;
-    __syncthreads();
-    int chunk_total = 0;
-    for (int w = 0; w < 16; ++w) chunk_total += wsum[w];
-    carry += chunk_total;
-    __syncthreads();
-  }
-  for (int e = tid; e < nb1; e += blockDim.x) {
-    if (e < nb) {
-      counts[e] = tot[e];
-      offsets[e] = start[e] + tot[e];
-    }
-    for (int b = 0; b < nblk; ++b) hist[static_cast<int64_t>(b) * nb1 + e] += start[e];
+  // Inclusive scan over the real buckets (nb <= 1024: one pass).
+  const int v = tid < nb ? tot[tid] : 0;
+  const int incl = wave_inclusive_scan(v);
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  int wprefix = 0;
+  for (int w = 0; w < wave; ++w) wprefix += wsum[w];
+  if (tid < nb) {
+    counts[tid] = v;
+    offsets[tid] = wprefix + incl;
   }
 }
 
 __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(const int64_t* __restrict__ ids, int S,
                                                                         int64_t divisor, int nb,
-                                                                        const int32_t* __restrict__ base,
+                                                                        const int32_t* __restrict__ col_prefix,
+                                                                        const int32_t* __restrict__ counts,
+                                                                        const int32_t* __restrict__ offsets,
                                                                         int32_t* __restrict__ perm,
                                                                         int32_t* __restrict__ pos_of_slot) {
   __shared__ int running[kMaxBuckets + 1];
   __shared__ int wave_cnt[kPermThreads / kWave][kMaxBuckets + 1];
   const int nb1 = nb + 1;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int begin = blockIdx.x * kChunk;
+  const int end = min(begin + kChunk, S);
+  // Every round's ids in flight before the first round.
+  int64_t id[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r) {
+    const int s = begin + r * kPermThreads + threadIdx.x;
+    id[r] = s < end ? ids[s] : -1;
+  }
   for (int i = threadIdx.x; i < nb1; i += kPermThreads) {
-    running[i] = base[static_cast<int64_t>(blockIdx.x) * nb1 + i];
+    const int bucket_start = i < nb ? offsets[i] - counts[i] : offsets[nb - 1];
+    running[i] = col_prefix[static_cast<int64_t>(blockIdx.x) * nb1 + i] + bucket_start;
 #pragma unroll
     for (int w = 0; w < kPermThreads / kWave; ++w) wave_cnt[w][i] = 0;
   }
@@ -111,12 +129,13 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(const int
   int nbits = 1;
   while ((1 << nbits) < nb1) ++nbits;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int begin = blockIdx.x * kChunk;
-  const int end = min(begin + kChunk, S);
-  for (int r0 = begin; r0 < end; r0 += kPermThreads) {
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r) {
+    const int r0 = begin + r * kPermThreads;
+    if (r0 >= end) break;
     const int s = r0 + threadIdx.x;
     const bool live = s < end;
-    const int key = live ? bucket_of(ids[s], divisor, nb) : 0;
+    const int key = live ? bucket_of(id[r], divisor, nb) : 0;
     // Lanes holding the same key: intersect one ballot per key bit.
     unsigned long long match = __ballot(live);
 #pragma unroll 1
@@ -285,8 +304,8 @@ extern "C" int moe_permute_fwd(const void* hidden, int64_t T, int64_t H, const i
   int rc = launch_status("moe_permute_fwd(scan)");
   if (rc) return rc;
   if (nblk == 0) return MOE_OK;
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nblk), dim3(kPermThreads), 0, st, ids, S, divisor, nb, hist, perm,
-                     pos_of_slot);
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nblk), dim3(kPermThreads), 0, st, ids, S, divisor, nb, hist, counts,
+                     offsets, perm, pos_of_slot);
   rc = launch_status("moe_permute_fwd(scatter)");
   if (rc) return rc;
   if (permuted) {
