@@ -22,6 +22,7 @@
  *   aux loss   TF/models/qwen3_moe/modeling_qwen3_moe.py:514-593,
  *              parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280
  *   dispatch   parallel/parallel/engine/model_parallel/token_dispatch.py:78-174
+ *   FSDP grads parallel/parallel/engine/_dp_param_unit.py:268-277,395-417
  */
 #ifndef MOE_MI355X_H
 #define MOE_MI355X_H
@@ -256,6 +257,22 @@ int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs,
                            int64_t G, int64_t M, int64_t N, int64_t K,
                            void* dw, int dw_is_f32, int accumulate,
                            void* stream);
+
+/* moe_grouped_gemm_wgrad with group g's [N,K] block written into an FSDP
+ * unit's rank-major gradient bucket instead of a dense [G,N,K] tensor: at
+ * element (g / bucket_rows) * bucket_stride + (g % bucket_rows) * N * K from
+ * `bucket`.  This replaces the copy of a parameter's full gradient into the
+ * reduce-scatter input in DPParamUnit.start_gradient_reduction
+ * (parallel/parallel/engine/_dp_param_unit.py:395-417): `bucket` points at the
+ * parameter's bucket_offset in rank 0's chunk, bucket_rows is its padded
+ * rows per rank, ceil(G / world_size) (:200), and bucket_stride the unit's
+ * bucket_numel (:268-277).  Padding rows are not written (the reference
+ * zero-fills the bucket); bucket_stride must keep rank chunks 16-byte aligned. */
+int moe_grouped_gemm_wgrad_bucket(const void* dc, const void* a,
+                                  const int32_t* offs, int64_t G, int64_t M,
+                                  int64_t N, int64_t K, void* bucket,
+                                  int64_t bucket_rows, int64_t bucket_stride,
+                                  int dw_is_f32, int accumulate, void* stream);
 
 #ifdef __cplusplus
 }

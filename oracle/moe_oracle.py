@@ -16,6 +16,9 @@ It restates, on the CPU, the reference path's arithmetic:
   * token dispatch   parallel/parallel/engine/model_parallel/token_dispatch.py:86-174
   * block-input norm TF/models/qwen3_moe/modeling_qwen3_moe.py:294-299 (Qwen3MoeRMSNorm, the
                      post_attention_layernorm applied before the MoE block at :345)
+  * FSDP grad bucket parallel/parallel/engine/_dp_param_unit.py:200-202 (padded rows),
+                     :268-277 (bucket layout), :395-417 (rank-major packing of the
+                     reduce-scatter input)
 where TF/ is transformers (the reference pins 5.14.1, uv.lock:2274-2275; the
 5.15.0 installed here is what the golden vectors were generated with).
 Integer work (sort keys, permutations, counts, splits) is numpy; floating
@@ -302,3 +305,45 @@ def reference_step(leaves, d_out, *, top_k, norm_topk_prob, aux_coef, compute_dt
     aux = load_balancing_loss((logits,), rw.shape[0], top_k)
     torch.autograd.backward([out, aux], [d_out.to(out.dtype), torch.tensor(aux_coef)])
     return out
+
+
+# ----------------------------------------------------------------- FSDP gradient bucket
+
+
+def fsdp_bucket_layout(shapes, world_size: int):
+    """Per parameter (padded_rows, bucket_offset, padded_numel), and the unit's
+    bucket_numel.  padded_rows = ceil(rows / world) (_dp_param_unit.py:200);
+    parameters take consecutive flat offsets in unit order (:268-277)."""
+    layout, offset = [], 0
+    for shape in shapes:
+        padded_rows = (shape[0] + world_size - 1) // world_size
+        padded_numel = padded_rows
+        for size in shape[1:]:
+            padded_numel *= size
+        layout.append((padded_rows, offset, padded_numel))
+        offset += padded_numel
+    return layout, offset
+
+
+def fsdp_pack_grads(grads, world_size: int, dtype=None, shapes=None):
+    """The reduce-scatter input [world, bucket_numel] of one FSDP unit: rank r's
+    chunk holds rows [r * padded_rows, ...) of every parameter's gradient at the
+    parameter's offset, zeros elsewhere (_dp_param_unit.py:395-417).  A None
+    gradient (its parameter's shape from ``shapes``) leaves its slots zero."""
+    if shapes is None:
+        shapes = [tuple(g.shape) for g in grads]
+    layout, numel = fsdp_bucket_layout(shapes, world_size)
+    first = next(g for g in grads if g is not None)
+    bucket = torch.zeros(world_size, numel, dtype=dtype or first.dtype)
+    for g, (padded_rows, offset, padded_numel) in zip(grads, layout):
+        if g is None:
+            continue
+        for rank in range(world_size):
+            start = rank * padded_rows
+            rows = min(padded_rows, max(g.shape[0] - start, 0))
+            if not rows:
+                continue
+            dest = bucket[rank].narrow(0, offset, padded_numel).view(padded_rows, *g.shape[1:])
+            dest[:rows].copy_(g.narrow(0, start, rows))
+    return bucket
+

@@ -9,6 +9,7 @@ and as drop-ins for the reference's interfaces.
 
 from .aux_loss import load_balancing_loss_func, sequence_parallel_load_balancing_loss
 from .checkpoint import MoeLayerWeights, load_moe_layer
+from .fsdp_bucket import GradBucketLayout, experts_backward_into_bucket, pack_gradient
 from .norm_router import norm_router_aux
 from .expert_parallel import (
     ExpertPartition,
@@ -33,6 +34,7 @@ __all__ = [
     "EXPERTS_IMPLEMENTATION",
     "ExpertPartition",
     "Experts",
+    "GradBucketLayout",
     "MoeConfig",
     "MoeLayerWeights",
     "ReplicatedTokenExpertParallel",
@@ -40,9 +42,11 @@ __all__ = [
     "SparseMoeBlock",
     "TokenDispatcher",
     "TopKRouter",
+    "experts_backward_into_bucket",
     "load_balancing_loss_func",
     "load_moe_layer",
     "norm_router_aux",
+    "pack_gradient",
     "local_expert_range",
     "mi355x_experts_forward",
     "register_experts_implementation",

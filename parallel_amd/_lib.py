@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_grouped_gemm_dgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "moe_grouped_gemm_dgrad_swiglu_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "moe_grouped_gemm_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I, _I, _P]),
+    "moe_grouped_gemm_wgrad_bucket": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I, _I, _P]),
     "moe_rmsnorm_fwd": (_I, [_P, _P, _I64, _I64, ctypes.c_float, _P, _P, _P]),
     "moe_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),

@@ -69,6 +69,11 @@ struct GemmParams {
   int k_splits, k_chunk;  // MG without groups: split the reduction, partial outputs stacked
   int64_t split_stride;   // elements between split partials of C
   int chunk_rows;         // KG without offs and G > 1: group g = rows [g*chunk_rows, ...)
+  // KG into a rank-major bucket (0 = plain): group g's output starts
+  // (g / bucket_rows) * bucket_stride + (g % bucket_rows) * stride_cg
+  // elements into C instead of g * stride_cg.
+  int bucket_rows;
+  int64_t bucket_stride;
 };
 
 // ---------------------------------------------------------------- helpers
@@ -666,7 +671,9 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
     // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
     const int esize = (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) ? 4 : 2;
-    const int64_t c_base = (MODE == MODE_KG) ? static_cast<int64_t>(t.g) * p.stride_cg
+    const int64_t c_base = (MODE == MODE_KG) ? (p.bucket_rows ? static_cast<int64_t>(t.g / p.bucket_rows) * p.bucket_stride +
+                                                                 static_cast<int64_t>(t.g % p.bucket_rows) * p.stride_cg
+                                                               : static_cast<int64_t>(t.g) * p.stride_cg)
                          : (EPI == EPI_F32)  ? static_cast<int64_t>(t.split) * p.split_stride
                                              : 0;
     const __amdgpu_buffer_rsrc_t rsC = make_rsrc(uniform_ptr(static_cast<char*>(p.C) + c_base * esize), p.c_bytes);
@@ -1204,12 +1211,13 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   return launch_status("moe_grouped_gemm_dgrad_swiglu_bwd (swiglu)");
 }
 
-extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
-                                      int64_t N, int64_t K, void* dw, int dw_is_f32, int accumulate, void* stream) {
+namespace {
+int wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K, void* dw,
+          int dw_is_f32, int accumulate, int64_t bucket_rows, int64_t bucket_stride, void* stream, const char* name) {
   // dw[g][N,K] = dc[rows g, N]^T . a[rows g, K]: GEMM-internal output N x K, reduction over rows.
   int rc = check_common(dc, a, offs, G, M, N, K);
   if (rc) return rc;
-  MOE_REQUIRE(dw && aligned16(dw), MOE_ERR_INVALID, "grouped gemm wgrad: bad output pointer");
+  MOE_REQUIRE(dw && aligned16(dw), MOE_ERR_INVALID, "%s: bad output pointer", name);
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(dc);
   p.B = static_cast<const bf16_t*>(a);
@@ -1227,6 +1235,28 @@ extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32
   p.stride_cg = N * K;
   p.accumulate = accumulate ? 1 : 0;
   p.chunk_rows = static_cast<int>(M);
-  if ((rc = set_bytes(p, M * N * 2, M * K * 2, N * K * (dw_is_f32 ? 4 : 2), "moe_grouped_gemm_wgrad"))) return rc;
-  return launch<MODE_KG, false, EPI_WGRAD, BigTile>(p, as_stream(stream), "moe_grouped_gemm_wgrad");
+  p.bucket_rows = static_cast<int>(bucket_rows);
+  p.bucket_stride = bucket_stride;
+  if ((rc = set_bytes(p, M * N * 2, M * K * 2, N * K * (dw_is_f32 ? 4 : 2), name))) return rc;
+  return launch<MODE_KG, false, EPI_WGRAD, BigTile>(p, as_stream(stream), name);
+}
+}  // namespace
+
+extern "C" int moe_grouped_gemm_wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
+                                      int64_t N, int64_t K, void* dw, int dw_is_f32, int accumulate, void* stream) {
+  return wgrad(dc, a, offs, G, M, N, K, dw, dw_is_f32, accumulate, 0, 0, stream, "moe_grouped_gemm_wgrad");
+}
+
+extern "C" int moe_grouped_gemm_wgrad_bucket(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M,
+                                             int64_t N, int64_t K, void* bucket, int64_t bucket_rows,
+                                             int64_t bucket_stride, int dw_is_f32, int accumulate, void* stream) {
+  const char* name = "moe_grouped_gemm_wgrad_bucket";
+  MOE_REQUIRE(bucket_rows >= 1 && bucket_rows <= G, MOE_ERR_INVALID, "%s: bucket_rows=%lld outside [1, G=%lld]", name,
+              (long long)bucket_rows, (long long)G);
+  MOE_REQUIRE(bucket_stride >= bucket_rows * N * K, MOE_ERR_INVALID,
+              "%s: bucket_stride=%lld smaller than one rank's %lld x %lld x %lld shard", name,
+              (long long)bucket_stride, (long long)bucket_rows, (long long)N, (long long)K);
+  MOE_REQUIRE((bucket_stride * (dw_is_f32 ? 4 : 2)) % 16 == 0, MOE_ERR_UNSUPPORTED,
+              "%s: rank chunks of %lld elements are not 16-byte aligned", name, (long long)bucket_stride);
+  return wgrad(dc, a, offs, G, M, N, K, bucket, dw_is_f32, accumulate, bucket_rows, bucket_stride, stream, name);
 }

@@ -457,11 +457,13 @@ def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj):
             hidden.new_empty(S, H), hidden.new_empty(S, **i32), hidden.new_empty(E, **i32))
 
 
-@torch.library.custom_op(f"{LIB}::experts_bwd", mutates_args=())
-def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
-                pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor,
-                offsets: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(d_hidden [T,H], d_weights [T,k] f32, d_gate_up_proj, d_down_proj)."""
+def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
+                        pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor, offsets: Tensor,
+                        wgrad) -> tuple[Tensor, Tensor, object, object]:
+    """The expert backward's launches; ``wgrad(name, dc, a, n, k)`` issues the
+    weight gradient dW[g][n,k] = dc[rows of g]ᵀ · a[rows of g] of projection
+    ``name`` ("gate_up_proj", then "down_proj") and returns whatever stands for
+    it.  Returns (d_hidden [T,H], d_weights [T,k] f32, wgrad's two results)."""
     T, k = top_k_weights.shape
     E, I2, H = gate_up_proj.shape
     I = I2 // 2
@@ -487,13 +489,29 @@ def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down
     d_hidden = torch.empty(T, H, dtype=BF16, device=dev)
     call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, None, ptr(d_hidden), s,
          tag="permute_bwd")
-    d_gu = torch.empty_like(gate_up_proj)
-    call("moe_grouped_gemm_wgrad", ptr(d_pre), ptr(xp), ptr(offsets), E, S, 2 * I, H, ptr(d_gu), 0, 0, s,
-         tag="up_wgrad")
-    d_down = torch.empty_like(down_proj)
-    call("moe_grouped_gemm_wgrad", ptr(dy), ptr(act), ptr(offsets), E, S, H, I, ptr(d_down), 0, 0, s,
-         tag="down_wgrad")
+    d_gu = wgrad("gate_up_proj", d_pre, xp, 2 * I, H)
+    d_down = wgrad("down_proj", dy, act, H, I)
     return d_hidden, d_w, d_gu, d_down
+
+
+@torch.library.custom_op(f"{LIB}::experts_bwd", mutates_args=())
+def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
+                pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor,
+                offsets: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d_hidden [T,H], d_weights [T,k] f32, d_gate_up_proj, d_down_proj)."""
+    E = gate_up_proj.shape[0]
+    S = xp.shape[0]
+    s = _stream(d_out)
+    params = {"gate_up_proj": gate_up_proj, "down_proj": down_proj}
+
+    def wgrad(name, dc, a, n, k):
+        dw = torch.empty_like(params[name])
+        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s,
+             tag="up_wgrad" if name == "gate_up_proj" else "down_wgrad")
+        return dw
+
+    return experts_bwd_kernels(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets,
+                               wgrad)
 
 
 @experts_bwd.register_fake
