@@ -863,7 +863,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       barrier();
       dma_prepare(dstage);
       if (n_act > 0) {
+        // Issue priority while the wave feeds its MFMAs, so that on a shared
+        // SIMD the wave with matrix work ready goes before the other wave's
+        // address arithmetic and epilogue (0.4-0.6% on the expert GEMMs).
+        __builtin_amdgcn_s_setprio(1);
         compute(n_act, ring + cstage * STAGE_BYTES);
+        __builtin_amdgcn_s_setprio(0);
       } else {
 #pragma unroll
         for (int j = 0; j < LPW; ++j) dma_fire(j);
