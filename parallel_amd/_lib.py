@@ -123,12 +123,16 @@ def check(rc: int, what: str) -> None:
 class KernelTimer:
     """Optional per-entry-point HIP event timing on torch's current stream.
 
-    When enabled, every ``call`` records a start/end event pair around the
-    entry point on the current stream (the stream the kernels are launched
-    on); ``durations_ms()`` resolves them after a synchronisation."""
+    When enabled, every ``call`` (or, with ``only`` set, every call whose tag
+    is in ``only``) records a start/end event pair around the entry point on
+    the current stream (the stream the kernels are launched on);
+    ``durations_ms()`` resolves them after a synchronisation.  An event pair
+    costs several microseconds of stream time, so a timed region should
+    instrument only the launches it needs."""
 
     def __init__(self):
         self.enabled = False
+        self.only: set[str] | None = None
         self.events: dict[str, list] = {}
 
     def reset(self) -> None:
@@ -146,7 +150,7 @@ def call(name: str, *args, tag: str | None = None) -> None:
 
     ``tag`` names the launch for KernelTimer (one entry point serves several
     GEMMs of different shapes)."""
-    if TIMER.enabled:
+    if TIMER.enabled and (TIMER.only is None or (tag or name) in TIMER.only):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
