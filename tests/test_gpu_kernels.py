@@ -21,8 +21,12 @@ def gen(seed):
 
 # ------------------------------------------------------------------- router
 
+# E spans every experts-per-lane instantiation (1, 2, 4, 8, 16; 200 leaves the
+# last lane chunk partly empty) and k the specialised (1, 2, 4, 6, 8) and the
+# generic (3, 5, 16) forms.
 ROUTER_CASES = [(512, 8, 2, True), (4096, 128, 8, True), (1000, 128, 8, False), (257, 64, 4, True),
-                (64, 1024, 16, True), (33, 3, 3, False)]
+                (64, 1024, 16, True), (33, 3, 3, False), (300, 200, 6, True), (128, 384, 1, False),
+                (96, 512, 5, True)]
 
 
 @pytest.mark.parametrize("T,E,k,norm", ROUTER_CASES)
@@ -58,9 +62,9 @@ def test_router_logits_match_fp32(T, H, E):
     assert not ((idx.cpu() != ref_i).any(1) & ~ties).any()
 
 
-@pytest.mark.parametrize("norm", [True, False])
-def test_router_backward_matches_autograd(norm):
-    T, H, E, k = 384, 256, 16, 4
+@pytest.mark.parametrize("norm,E,k", [(True, 16, 4), (False, 16, 4), (True, 200, 6), (False, 384, 1)])
+def test_router_backward_matches_autograd(norm, E, k):
+    T, H = 384, 256
     x = torch.randn(T, H, generator=gen(3)).to(BF)
     w = (torch.randn(E, H, generator=gen(4)) * 0.05).to(BF)
     d_scores = torch.randn(T, k, generator=gen(5))
@@ -82,7 +86,8 @@ def test_router_backward_matches_autograd(norm):
 # ------------------------------------------------------------------ aux loss
 
 
-@pytest.mark.parametrize("T,E,k,masked", [(512, 8, 2, False), (4096, 128, 8, False), (2 * 96, 64, 6, True)])
+@pytest.mark.parametrize("T,E,k,masked", [(512, 8, 2, False), (4096, 128, 8, False), (2 * 96, 64, 6, True),
+                                           (2 * 150, 200, 6, True), (256, 384, 1, False), (128, 1024, 16, False)])
 def test_aux_loss_forward_backward(T, E, k, masked):
     logits = torch.randn(T, E, generator=gen(T)) * 2
     mask = None
