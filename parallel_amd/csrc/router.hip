@@ -8,6 +8,8 @@
 // Reference arithmetic: TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267
 // (router) and :514-593 (load_balancing_loss_func); the one-rank SP variant is
 // parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280.
+#include <type_traits>
+
 #include "gemm.h"
 
 namespace moe {

@@ -14,6 +14,9 @@ Ops (namespace ``parallel_amd``):
   combine_rows_fwd / _bwd          gather-form index_add back to source tokens
   rmsnorm_fwd / rmsnorm_bwd        post_attention_layernorm of the block input (+ backward)
   router_aux_fwd                   router_fwd plus the aux loss from the same top-k
+
+experts_bwd_kernels issues the expert backward's launches with a caller-chosen
+weight-gradient target (fsdp_bucket uses it to write into an FSDP bucket).
 """
 
 from __future__ import annotations
