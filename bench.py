@@ -178,7 +178,8 @@ def profile_summary(args) -> int:
     for r, tag in zip(trace, tags):
         disp[(tag or "-", r["Kernel_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     grand = sum(sum(v) for v in disp.values())
-    lines = [f"# rocprofv3 kernel statistics, workload {w.name} ({args.steps_profiled} timed + warm-up steps)",
+    lines = [f"# rocprofv3 kernel statistics, workload {w.name} ({args.steps_profiled} timed steps plus the warm-up "
+             f"and instrumented steps)",
              f"# command: {cmd.splitlines()[0] if cmd else '(not recorded)'}",
              f"# {'tag':16s} {'calls':>6s} {'avg_us':>10s} {'total_us':>11s} {'pct':>6s}  kernel"]
     per_tag = defaultdict(lambda: [0.0, 0])
@@ -294,7 +295,8 @@ def main() -> int:
     ap.add_argument("--pmc-write")
     ap.add_argument("--cal-fetch")
     ap.add_argument("--cal-write")
-    ap.add_argument("--pmc-calls", type=int, default=3, help="entry-point calls in the --pmc runs (warm-up + steps)")
+    ap.add_argument("--pmc-calls", type=int, default=6,
+                    help="entry-point calls in the --pmc runs: warm-up + instrumented + timed steps (1 + 3 + 2)")
     ap.add_argument("--steps-profiled", type=int, default=10)
     ap.add_argument("--profile-commands", help="the rocprofv3 command lines, one per line, recorded in the summaries")
     args = ap.parse_args()
