@@ -85,6 +85,17 @@ int moe_router_topk_bwd(const float* logits, const int64_t* indices,
                         int norm_topk_prob, float* d_logits, int accumulate,
                         void* d_logits_bf16, void* stream);
 
+/* moe_router_topk_bwd for a caller that only needs the bf16 d_logits (the
+ * router GEMMs' input): d_logits_bf16 = bf16(g + d_add) with g the top-k /
+ * softmax backward and d_add an optional f32 [T,E] gradient that reaches the
+ * logits by another path (the aux loss's); d_add is only read, so the
+ * caller's tensor need not be copied.  Same reference as moe_router_topk_bwd. */
+int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices,
+                             const float* d_scores, const float* d_add,
+                             int64_t T, int64_t E, int64_t k,
+                             int norm_topk_prob, void* d_logits_bf16,
+                             void* stream);
+
 /* Backward of the router GEMM (F.linear, modeling_qwen3_moe.py:260) from
  * bf16 d_logits[T,E]: dx[T,H] = d_logits · wr (bf16) and dwr[E,H] =
  * d_logitsᵀ · x (bf16, reduced in f32 over row chunks held in the workspace). */

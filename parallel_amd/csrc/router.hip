@@ -244,11 +244,13 @@ __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, 
   }
 }
 
-// d_logits = p * (dp - <dp, p>), dp scattered from the (renormalised) top-k.
+// d_logits = p * (dp - <dp, p>) (+ d_add), dp scattered from the (renormalised)
+// top-k; the f32 result goes to d_logits and its bf16 rounding to
+// d_logits_bf16 (either may be null).  d_add may alias d_logits.
 template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ indices, const float* __restrict__ d_scores, int T,
-    int E, int k_rt, int norm, float* __restrict__ d_logits, int accumulate, bf16_t* __restrict__ d_logits_bf16) {
+    int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
   const int lane = threadIdx.x & (kWave - 1);
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
   for (int r = 0; r < KM; ++r)
     if (r < k) c += dv[r] * pv[r];
 
-  float* drow = d_logits + static_cast<int64_t>(t) * E;
+  const int64_t base = static_cast<int64_t>(t) * E;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int e = lane + j * kWave;
@@ -305,9 +307,9 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
         if (r < k && idx[r] == e) dp += dv[r];
       float p = expf(v[j] - st.max) * inv_sum;
       float g = p * (dp - c);
-      if (accumulate) g += drow[e];
-      drow[e] = g;
-      if (d_logits_bf16) d_logits_bf16[static_cast<int64_t>(t) * E + e] = f32_to_bf16(g);
+      if (d_add) g += d_add[base + e];
+      if (d_logits) d_logits[base + e] = g;
+      if (d_logits_bf16) d_logits_bf16[base + e] = f32_to_bf16(g);
     }
   }
 }
@@ -544,9 +546,26 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
     hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       d_logits, accumulate ? 1 : 0, static_cast<bf16_t*>(d_logits_bf16));
+                       accumulate ? d_logits : nullptr, d_logits, static_cast<bf16_t*>(d_logits_bf16));
   });
   return launch_status("moe_router_topk_bwd");
+}
+
+extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
+                                        const float* d_add, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                                        void* d_logits_bf16, void* stream) {
+  int rc = check_router(T, E, k);
+  if (rc) return rc;
+  MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "router topk bwd bf16: null pointer");
+  if (T == 0) return MOE_OK;
+  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
+  with_npl_k(E, k, [&](auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16));
+  });
+  return launch_status("moe_router_topk_bwd_bf16");
 }
 
 extern "C" size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E) {

@@ -124,16 +124,15 @@ def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_log
     E = weight.shape[0]
     k = indices.shape[1]
     s = _stream(x)
-    if d_logits is not None:
-        dl = d_logits.float().contiguous().clone()
-    else:
-        dl = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    d_add = None if d_logits is None else d_logits.float().contiguous()
     dl_bf16 = torch.empty(T, E, dtype=BF16, device=x.device)
     if d_scores is None:
         d_scores = torch.zeros(T, k, dtype=torch.float32, device=x.device)
     d_scores = d_scores.float().contiguous()
-    call("moe_router_topk_bwd", ptr(logits), ptr(indices), ptr(d_scores), T, E, k, int(norm_topk_prob), ptr(dl),
-         int(d_logits is not None), ptr(dl_bf16), s, tag="router_topk_bwd")
+    # Only the bf16 d_logits feeds the GEMMs; the incoming logits gradient is
+    # read, not copied.
+    call("moe_router_topk_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
+         int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
     dx = torch.empty(T, H, dtype=BF16, device=x.device)
     dw = torch.empty(E, H, dtype=weight.dtype, device=x.device)
     ws = _ws(_lib.load().moe_router_logits_bwd_workspace_bytes(T, H, E), x.device)
