@@ -205,3 +205,29 @@ def test_full_c2_forward_properties_and_sampled_tokens():
     sample = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(0))[:48]
     ref = O.experts_grouped(x.cpu()[sample], idx.cpu()[sample], scores.cpu()[sample], gu.cpu(), dn.cpu())
     close_bf16(out1.cpu()[sample], ref, "c2 sampled tokens")
+
+
+def test_experts_concentrated_routing():
+    """Every token routes to the same k experts: k groups of T rows (several
+    evenly split m-tiles each) and E - k empty experts, forward and backward,
+    against the oracle's grouped experts."""
+    T, H, E, k, I = 1100, 256, 16, 4, 128
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(T, H, generator=g).to(BF)
+    idx = torch.tensor([3, 7, 8, 15]).repeat(T, 1)
+    scores = torch.softmax(torch.randn(T, k, generator=g), -1)
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(BF)
+    dn = (torch.randn(E, H, I, generator=g) * 0.05).to(BF)
+    d_out = torch.randn(T, H, generator=g).to(BF)
+    leaves = [t.clone().requires_grad_() for t in (x, scores, gu, dn)]
+    ref = O.experts_grouped(leaves[0], idx, leaves[1], leaves[2], leaves[3])
+    ref.backward(d_out)
+    dl = [t.to(DEV).requires_grad_() for t in (x, scores, gu, dn)]
+    out = ops.experts(dl[0], idx.to(DEV), dl[1], dl[2], dl[3])
+    out.backward(d_out.to(DEV))
+    torch.cuda.synchronize()
+    close_bf16(out, ref, "concentrated out")
+    for name, a, b in zip(("dx", "d_scores", "d_gate_up", "d_down"), dl, leaves):
+        close_bf16(a.grad, b.grad, f"concentrated {name}")
+    unused = [e for e in range(E) if e not in (3, 7, 8, 15)]
+    assert not dl[2].grad[unused].any() and not dl[3].grad[unused].any(), "experts without routes get zero dW"

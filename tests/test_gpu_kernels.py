@@ -209,6 +209,7 @@ GEMM_CASES = [
     ("ragged", [7, 0, 0, 130, 64, 1], 200, 72),
     ("single", [1000], 128, 256),
     ("split", [770, 257, 33], 1280, 64),  # m-tiles of 224/224/224/98 and 160/97 rows
+    ("skewed", [0, 0, 3000, 0, 1, 0, 0, 0], 1536, 128),  # one group of 12 m-tiles, the rest empty or one row
 ]
 
 
