@@ -84,7 +84,9 @@ template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ void argmax_step(float& v, int& i) {
   float ov = dpp_move<CTRL, ROW_MASK>(v, v);
   int oi = dpp_move_i<CTRL, ROW_MASK>(i, i);
-  bool take = ov > v || (ov == v && oi < i);
+  // Bitwise, not short-circuit: the compiler would otherwise branch on each
+  // comparison (exec-mask save/restore around every step).
+  const bool take = (ov > v) | ((ov == v) & (oi < i));
   v = take ? ov : v;
   i = take ? oi : i;
 }

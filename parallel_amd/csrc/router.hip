@@ -1,9 +1,10 @@
 // Router top-k softmax and the Switch load-balancing loss (gfx950).
 //
-// One 64-lane wave per token: lane l holds experts l, l+64, ... in registers,
-// so softmax statistics and the k-way selection are wave reductions with no
-// LDS.  Selection is on the logits (softmax is monotone), largest first, ties
-// to the lower expert index; probabilities are exp(l - max) / sum in fp32.
+// A token's logits sit in the registers of 16 lanes (up to 256 experts, four
+// tokens per wave) or of a whole wave, so softmax statistics and the k-way
+// selection are DPP reductions with no LDS.  Selection is on the logits
+// (softmax is monotone), largest first, ties to the lower expert index;
+// probabilities are exp(l - max) / sum in fp32.
 //
 // Reference arithmetic: TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267
 // (router) and :514-593 (load_balancing_loss_func); the one-rank SP variant is
@@ -18,18 +19,69 @@ constexpr int kMaxPerLane = 16;  // E <= 1024
 constexpr int kMaxTopK = 16;
 constexpr int kRouterWaves = 4;  // waves per block
 
-// The kernels are instantiated per NPL (experts per lane, E <= 64 NPL, a power
-// of two) and KT (top-k; 0 = any k up to kMaxTopK), so that the per-lane loops
-// have fixed trip counts.  Items of lanes past E read as -inf and are never
-// selected; the arithmetic is that of any NPL large enough for E.
+// Token layout.  A token occupies LPT consecutive lanes: one 16-lane DPP row
+// (E <= 256, four tokens per wave) or the whole wave (E <= 1024).  Lane `sub`
+// of a token holds experts sub, sub + LPT, ... (NPL of them, a power of two),
+// so the softmax statistics and the k-way selection are reductions over the
+// token's lanes with no LDS.  With 16-lane rows each reduction is 4 DPP steps
+// serving 4 tokens at once; one token per wave spent about 850 VALU
+// instructions per token, most of them in 6-step wave reductions.
+// The kernels are instantiated per (LPT, NPL) and KT (top-k; 0 = any k up to
+// kMaxTopK), so that the per-lane loops have fixed trip counts.  Items past E
+// read as -inf and are never selected; the arithmetic is that of any NPL
+// large enough for E.
+template <int LPT>
+struct Tok {
+  static_assert(LPT == 16 || LPT == kWave, "a token is one DPP row or one wave");
+  static constexpr int kPerBlock = kRouterWaves * (kWave / LPT);
+  __device__ static int sub() { return threadIdx.x & (LPT - 1); }
+  // The token's slot in the block (wave-major, then row).
+  __device__ static int slot() { return threadIdx.x / LPT; }
+};
+
+// Reductions over a token's lanes.  Every lane of the token gets the result,
+// bit for bit: each butterfly step combines a pair of lanes commutatively.
+template <int LPT>
+__device__ __forceinline__ float tok_max(float v) {
+  if constexpr (LPT == kWave) {
+    return wave_max(v);
+  } else {
+    v = fmaxf(v, dpp_move<dpp::kQuadXor1>(v, v));
+    v = fmaxf(v, dpp_move<dpp::kQuadXor2>(v, v));
+    v = fmaxf(v, dpp_move<dpp::kHalfMirror>(v, v));
+    return fmaxf(v, dpp_move<dpp::kMirror>(v, v));
+  }
+}
+template <int LPT>
+__device__ __forceinline__ float tok_sum(float v) {
+  if constexpr (LPT == kWave) {
+    return wave_sum(v);
+  } else {
+    v += dpp_move<dpp::kQuadXor1>(0.0f, v);
+    v += dpp_move<dpp::kQuadXor2>(0.0f, v);
+    v += dpp_move<dpp::kHalfMirror>(0.0f, v);
+    return v + dpp_move<dpp::kMirror>(0.0f, v);
+  }
+}
+template <int LPT>
+__device__ __forceinline__ void tok_argmax(float& v, int& i) {
+  if constexpr (LPT == kWave) {
+    wave_argmax(v, i);
+  } else {
+    argmax_step<dpp::kQuadXor1>(v, i);
+    argmax_step<dpp::kQuadXor2>(v, i);
+    argmax_step<dpp::kHalfMirror>(v, i);
+    argmax_step<dpp::kMirror>(v, i);
+  }
+}
 
 // Loads one token's logits; absent experts read as -inf.
-template <int NPL>
+template <int LPT, int NPL>
 __device__ __forceinline__ void load_row(const float* row, int E, float (&v)[NPL]) {
-  const int lane = threadIdx.x & (kWave - 1);
+  const int sub = Tok<LPT>::sub();
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int e = lane + j * kWave;
+    const int e = sub + j * LPT;
     v[j] = e < E ? row[e] : -INFINITY;
   }
 }
@@ -38,25 +90,25 @@ struct SoftmaxStats {
   float max, sum;
 };
 
-template <int NPL>
+template <int LPT, int NPL>
 __device__ __forceinline__ SoftmaxStats softmax_stats(const float (&v)[NPL]) {
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) m = fmaxf(m, v[j]);
-  m = wave_max(m);
+  m = tok_max<LPT>(m);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPL; ++j)
     if (v[j] != -INFINITY) s += expf(v[j] - m);
-  s = wave_sum(s);
+  s = tok_sum<LPT>(s);
   return {m, s};
 }
 
-// k-way selection: sel_idx/sel_logit are wave-uniform after the call.
-template <int NPL, int KM>
+// k-way selection: sel_idx/sel_logit are the same in all lanes of the token.
+template <int LPT, int NPL, int KM>
 __device__ __forceinline__ void select_topk(const float (&v)[NPL], int E, int k, int (&sel_idx)[KM],
                                             float (&sel_logit)[KM]) {
-  const int lane = threadIdx.x & (kWave - 1);
+  const int sub = Tok<LPT>::sub();
   unsigned taken = 0;  // bit j: item j of this lane already selected
 #pragma unroll
   for (int r = 0; r < KM; ++r) {
@@ -65,79 +117,104 @@ __device__ __forceinline__ void select_topk(const float (&v)[NPL], int E, int k,
       int bidx = 0x7fffffff;
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
-        const int e = lane + j * kWave;
+        const int e = sub + j * LPT;
         // Items are visited in increasing e, so ">" keeps the lower index on
         // ties; the first live item is always taken (covers -inf logits).
-        if (e < E && !(taken & (1u << j)) && (v[j] > best || bidx == 0x7fffffff)) {
-          best = v[j];
-          bidx = e;
-        }
+        // Bitwise operators keep the scan free of branches.
+        const bool take = (e < E) & !(taken & (1u << j)) & ((v[j] > best) | (bidx == 0x7fffffff));
+        best = take ? v[j] : best;
+        bidx = take ? e : bidx;
       }
-      wave_argmax(best, bidx);
+      tok_argmax<LPT>(best, bidx);
       sel_idx[r] = bidx;
       sel_logit[r] = best;
-      if (bidx != 0x7fffffff && (bidx & (kWave - 1)) == lane) taken |= 1u << (bidx / kWave);
+      if (bidx != 0x7fffffff && (bidx & (LPT - 1)) == sub) taken |= 1u << (bidx / LPT);
     }
   }
 }
 
 // Top-k probabilities of the selection, then the scores (renormalised with
-// `norm`) and indices written by lanes 0 .. k-1.
-template <int KM>
+// `norm`) and indices: lane r of the token takes selection r (r < k <= LPT),
+// and the renormalising total is a sum over the token's lanes.
+template <int LPT, int KM>
 __device__ __forceinline__ void write_topk(const SoftmaxStats& st, const int (&sel)[KM], const float (&sl)[KM], int k,
                                            int norm, float* __restrict__ scores, int64_t* __restrict__ indices,
                                            int64_t t) {
-  const int lane = threadIdx.x & (kWave - 1);
-  float pv[KM];
-  float tot = 0.0f;
+  const int sub = Tok<LPT>::sub();
+  int my_idx = 0;
+  float my_logit = -INFINITY;
 #pragma unroll
   for (int r = 0; r < KM; ++r) {
-    if (r < k) {
-      pv[r] = expf(sl[r] - st.max) / st.sum;
-      tot += pv[r];
+    if (r < k && sub == r) {
+      my_idx = sel[r];
+      my_logit = sl[r];
     }
   }
-#pragma unroll
-  for (int r = 0; r < KM; ++r) {
-    if (r < k && lane == r) {
-      scores[t * k + r] = norm ? pv[r] / tot : pv[r];
-      indices[t * k + r] = sel[r];
-    }
+  const bool mine = sub < k;
+  const float pv = mine ? expf(my_logit - st.max) / st.sum : 0.0f;
+  const float tot = tok_sum<LPT>(pv);
+  if (mine) {
+    scores[t * k + sub] = norm ? pv / tot : pv;
+    indices[t * k + sub] = my_idx;
   }
 }
 
-template <int NPL, int KT>
+template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_fwd_kernel(const float* __restrict__ logits,
                                                                                 float* __restrict__ scores,
                                                                                 int64_t* __restrict__ indices, int T,
                                                                                 int E, int k_rt, int norm) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
-  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t >= T) return;
+  const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
+  if (t >= T) return;  // a whole token's lanes leave together
   float v[NPL];
-  load_row(logits + static_cast<int64_t>(t) * E, E, v);
-  const SoftmaxStats st = softmax_stats(v);
+  load_row<LPT>(logits + static_cast<int64_t>(t) * E, E, v);
+  const SoftmaxStats st = softmax_stats<LPT>(v);
   int sel[KM];
   float sl[KM];
-  select_topk(v, E, k, sel, sl);
-  write_topk(st, sel, sl, k, norm, scores, indices, t);
+  select_topk<LPT>(v, E, k, sel, sl);
+  write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t);
+}
+
+// The block's per-token aux terms (P_e, c_e, W) are summed over its token
+// slots in slot order into one partial row (shared by the fused router pass
+// and aux_partial_kernel, so that both give the same partials).
+template <int LPT, int NPL>
+__device__ __forceinline__ void aux_block_partial(float (*part)[2 * LPT * NPL + 1], const float (&P)[NPL],
+                                                  const float (&C)[NPL], float W, int E, float* __restrict__ out) {
+  const int sub = Tok<LPT>::sub(), slot = Tok<LPT>::slot();
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = sub + j * LPT;
+    if (e < E) {
+      part[slot][e] = P[j];
+      part[slot][E + e] = C[j];
+    }
+  }
+  if (sub == 0) part[slot][2 * E] = W;
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * E + 1; i += blockDim.x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < Tok<LPT>::kPerBlock; ++w) s += part[w][i];
+    out[i] = s;
+  }
 }
 
 // logits[t] = sum_s partials[s][t] (+ bias), then the top-k softmax of that row.
-// With aux_ws, also the aux-loss partials of the block's 4 tokens from the
+// With aux_ws, also the aux-loss partials of the block's tokens from the
 // same softmax and selection (the layout and arithmetic of aux_partial_kernel).
-template <int NPL, int KT>
+template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kernel(
     const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
     float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k_rt, int norm,
     const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
-  __shared__ float part[kRouterWaves][2 * kWave * NPL + 1];  // E <= 64 NPL
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * kRouterWaves + wave;
+  __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];  // E <= LPT NPL
+  const int sub = Tok<LPT>::sub();
+  const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
   if (t >= T && !aux_ws) return;
   const int64_t plane = static_cast<int64_t>(T) * E;
   float P[NPL], C[NPL];
@@ -157,7 +234,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
       for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          const int e = lane + j * kWave;
+          const int e = sub + j * LPT;
           q[u][j] = e < E ? partials[(sp + u) * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
         }
 #pragma unroll
@@ -168,13 +245,13 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
     for (; sp < splits; ++sp) {
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
-        const int e = lane + j * kWave;
+        const int e = sub + j * LPT;
         v[j] += e < E ? partials[sp * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
       }
     }
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
-      const int e = lane + j * kWave;
+      const int e = sub + j * LPT;
       if (e < E) {
         if (bias) v[j] += bias[e];
         logits[static_cast<int64_t>(t) * E + e] = v[j];
@@ -182,49 +259,31 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
         v[j] = -INFINITY;
       }
     }
-    const SoftmaxStats st = softmax_stats(v);
+    const SoftmaxStats st = softmax_stats<LPT>(v);
     int sel[KM];
     float sl[KM];
-    select_topk(v, E, k, sel, sl);
-    write_topk(st, sel, sl, k, norm, scores, indices, t);
+    select_topk<LPT>(v, E, k, sel, sl);
+    write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t);
     if (aux_ws) {
       const float w = token_weight ? token_weight[t] : 1.0f;
-      W = w;
+      // aux_partial_kernel's per-slot sums start from zero: 0 + term.
+      W = 0.0f + w;
       const float inv_sum = 1.0f / st.sum;
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
-        const int e = lane + j * kWave;
+        const int e = sub + j * LPT;
         if (e < E) {
-          P[j] = w * (expf(v[j] - st.max) * inv_sum);
+          P[j] = 0.0f + w * (expf(v[j] - st.max) * inv_sum);
           float cnt = 0.0f;
 #pragma unroll
           for (int r = 0; r < KM; ++r)
             if (r < k && sel[r] == e) cnt += 1.0f;
-          C[j] = w * cnt;
+          C[j] = 0.0f + w * cnt;
         }
       }
     }
   }  // t < T
-  if (aux_ws) {
-    // The block's 4 tokens, added in wave order (aux_partial_kernel's sums
-    // start from zero, so each wave's term is 0 + term).
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const int e = lane + j * kWave;
-      if (e < E) {
-        part[wave][e] = 0.0f + P[j];
-        part[wave][E + e] = 0.0f + C[j];
-      }
-    }
-    if (lane == 0) part[wave][2 * E] = 0.0f + W;
-    __syncthreads();
-    for (int i = threadIdx.x; i < 2 * E + 1; i += blockDim.x) {
-      float s = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kRouterWaves; ++w) s += part[w][i];
-      aux_ws[static_cast<int64_t>(blockIdx.x) * (2 * E + 1) + i] = s;
-    }
-  }
+  if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
 
 // out[i] = bf16(sum_c partials[c][i]) over n elements, fixed order.
@@ -247,19 +306,27 @@ __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, 
 // d_logits = p * (dp - <dp, p>) (+ d_add), dp scattered from the (renormalised)
 // top-k; the f32 result goes to d_logits and its bf16 rounding to
 // d_logits_bf16 (either may be null).  d_add may alias d_logits.
-template <int NPL, int KT>
+template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ indices, const float* __restrict__ d_scores, int T,
     int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  const int sub = Tok<LPT>::sub();
+  const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
   if (t >= T) return;
   float v[NPL];
   const float* row = logits + static_cast<int64_t>(t) * E;
-  load_row(row, E, v);
-  const SoftmaxStats st = softmax_stats(v);
+  const int64_t base = static_cast<int64_t>(t) * E;
+  load_row<LPT>(row, E, v);
+  // The added gradient is loaded with the logits, not after the arithmetic.
+  float add[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = sub + j * LPT;
+    add[j] = (d_add && e < E) ? d_add[base + e] : 0.0f;
+  }
+  const SoftmaxStats st = softmax_stats<LPT>(v);
   const float inv_sum = 1.0f / st.sum;
 
   int idx[KM];
@@ -296,10 +363,9 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
   for (int r = 0; r < KM; ++r)
     if (r < k) c += dv[r] * pv[r];
 
-  const int64_t base = static_cast<int64_t>(t) * E;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int e = lane + j * kWave;
+    const int e = sub + j * LPT;
     if (e < E) {
       float dp = 0.0f;
 #pragma unroll
@@ -307,7 +373,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
         if (r < k && idx[r] == e) dp += dv[r];
       float p = expf(v[j] - st.max) * inv_sum;
       float g = p * (dp - c);
-      if (d_add) g += d_add[base + e];
+      if (d_add) g += add[j];
       if (d_logits) d_logits[base + e] = g;
       if (d_logits_bf16) d_logits_bf16[base + e] = f32_to_bf16(g);
     }
@@ -316,44 +382,48 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
 
 // ------------------------------------------------------------------ aux loss
 
-constexpr int kAuxBlocksMax = 1024;  // per-block partial rows (a wave takes one token at a time)
+constexpr int kAuxBlocksMax = 1024;  // per-block partial rows (a token slot takes one token at a time)
 constexpr int kAuxGroups = 16;       // row groups of the partial reduction
 
-int aux_blocks(int64_t T) {
-  int64_t b = (T + kRouterWaves - 1) / kRouterWaves;
+// Lanes per token for E experts, and tokens per block.
+constexpr int lanes_per_token(int64_t E) { return E <= 16 * kMaxPerLane ? 16 : kWave; }
+constexpr int tokens_per_block(int64_t E) { return kRouterWaves * (kWave / lanes_per_token(E)); }
+
+int aux_blocks(int64_t T, int64_t E) {
+  const int64_t tpb = tokens_per_block(E);
+  int64_t b = (T + tpb - 1) / tpb;
   if (b < 1) b = 1;
   return static_cast<int>(b < kAuxBlocksMax ? b : kAuxBlocksMax);
 }
 
 // Per block partials: ws[b] = (P_0..P_{E-1}, c_0..c_{E-1}, W), fixed-order sums.
-template <int NPL, int KT>
+template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void aux_partial_kernel(const float* __restrict__ logits,
                                                                             const float* __restrict__ token_weight,
                                                                             int T, int E, int k_rt,
                                                                             float* __restrict__ ws) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
-  __shared__ float part[kRouterWaves][2 * kWave * NPL + 1];  // E <= 64 NPL
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];  // E <= LPT NPL
+  const int sub = Tok<LPT>::sub();
   float P[NPL], C[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
   float W = 0.0f;
-  const int waves_total = gridDim.x * kRouterWaves;
-  for (int t = blockIdx.x * kRouterWaves + wave; t < T; t += waves_total) {
+  const int stride = gridDim.x * Tok<LPT>::kPerBlock;
+  for (int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot(); t < T; t += stride) {
     float v[NPL];
-    load_row(logits + static_cast<int64_t>(t) * E, E, v);
-    const SoftmaxStats st = softmax_stats(v);
+    load_row<LPT>(logits + static_cast<int64_t>(t) * E, E, v);
+    const SoftmaxStats st = softmax_stats<LPT>(v);
     int sel[KM];
     float sl[KM];
-    select_topk(v, E, k, sel, sl);
+    select_topk<LPT>(v, E, k, sel, sl);
     const float w = token_weight ? token_weight[t] : 1.0f;
     W += w;
     const float inv_sum = 1.0f / st.sum;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
-      const int e = lane + j * kWave;
+      const int e = sub + j * LPT;
       if (e < E) {
         P[j] += w * (expf(v[j] - st.max) * inv_sum);
         float cnt = 0.0f;
@@ -364,22 +434,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_partial_kernel(const
       }
     }
   }
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    const int e = lane + j * kWave;
-    if (e < E) {
-      part[wave][e] = P[j];
-      part[wave][E + e] = C[j];
-    }
-  }
-  if (lane == 0) part[wave][2 * E] = W;
-  __syncthreads();
-  for (int i = threadIdx.x; i < 2 * E + 1; i += blockDim.x) {
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kRouterWaves; ++w) s += part[w][i];
-    ws[static_cast<int64_t>(blockIdx.x) * (2 * E + 1) + i] = s;
-  }
+  aux_block_partial<LPT>(part, P, C, W, E, ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
 
 // Column sums of the per-block partials in kAuxGroups row groups, fixed
@@ -438,18 +493,18 @@ __global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restr
   if (tid == 0) aux[0] = static_cast<float>(E) * terms[0];
 }
 
-template <int NPL>
+template <int LPT, int NPL>
 __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const float* __restrict__ logits,
                                                                         const float* __restrict__ token_weight,
                                                                         const float* __restrict__ stats,
                                                                         const float* __restrict__ d_aux, int T, int E,
                                                                         float* __restrict__ d_logits, int accumulate) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  const int sub = Tok<LPT>::sub();
+  const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
   if (t >= T) return;
   float v[NPL];
-  load_row(logits + static_cast<int64_t>(t) * E, E, v);
-  const SoftmaxStats st = softmax_stats(v);
+  load_row<LPT>(logits + static_cast<int64_t>(t) * E, E, v);
+  const SoftmaxStats st = softmax_stats<LPT>(v);
   const float inv_sum = 1.0f / st.sum;
   const float W = stats[E];
   const float w = token_weight ? token_weight[t] : 1.0f;
@@ -458,7 +513,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
   float dot = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int e = lane + j * kWave;
+    const int e = sub + j * LPT;
     p[j] = 0.0f;
     g[j] = 0.0f;
     if (e < E) {
@@ -467,11 +522,11 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
       dot += p[j] * g[j];
     }
   }
-  dot = wave_sum(dot);
+  dot = tok_sum<LPT>(dot);
   float* drow = d_logits + static_cast<int64_t>(t) * E;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int e = lane + j * kWave;
+    const int e = sub + j * LPT;
     if (e < E) {
       float d = p[j] * (g[j] - dot);
       drow[e] = accumulate ? drow[e] + d : d;
@@ -484,29 +539,48 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
 using namespace moe;
 
 namespace {
-// Instantiation for E experts (experts per lane rounded up to a power of two)
-// and top-k k (the specialised k, or the generic 0).
-template <class F>
+// Instantiation for E experts: lanes per token, experts per lane rounded up
+// to a power of two, and top-k k (the specialised k, or the generic 0).  The
+// selecting kernels take 16 lanes per token up to 256 experts (their k rounds
+// of reductions dominate); the backward kernels, which only stream a row in
+// and out, keep one wave per token so that more waves hide their loads.
+template <bool kWaveToken = false, class F>
 void with_npl(int64_t E, F&& f) {
-  const int64_t n = (E + kWave - 1) / kWave;
-  if (n <= 1) f(std::integral_constant<int, 1>{});
-  else if (n <= 2) f(std::integral_constant<int, 2>{});
-  else if (n <= 4) f(std::integral_constant<int, 4>{});
-  else if (n <= 8) f(std::integral_constant<int, 8>{});
-  else f(std::integral_constant<int, 16>{});
+  using L16 = std::integral_constant<int, 16>;
+  using L64 = std::integral_constant<int, kWave>;
+  static_assert(16 * kMaxPerLane == 256, "E <= 256 fits 16 lanes per token");
+  if (!kWaveToken && E <= 256) {
+    if (E <= 16) f(L16{}, std::integral_constant<int, 1>{});
+    else if (E <= 32) f(L16{}, std::integral_constant<int, 2>{});
+    else if (E <= 64) f(L16{}, std::integral_constant<int, 4>{});
+    else if (E <= 128) f(L16{}, std::integral_constant<int, 8>{});
+    else f(L16{}, std::integral_constant<int, 16>{});
+  } else {
+    if (E <= 64) f(L64{}, std::integral_constant<int, 1>{});
+    else if (E <= 128) f(L64{}, std::integral_constant<int, 2>{});
+    else if (E <= 256) f(L64{}, std::integral_constant<int, 4>{});
+    else if (E <= 512) f(L64{}, std::integral_constant<int, 8>{});
+    else f(L64{}, std::integral_constant<int, 16>{});
+  }
 }
-template <class F>
+template <bool kWaveToken = false, class F>
 void with_npl_k(int64_t E, int64_t k, F&& f) {
-  with_npl(E, [&](auto N) {
+  with_npl<kWaveToken>(E, [&](auto L, auto N) {
     switch (k) {
-      case 1: f(N, std::integral_constant<int, 1>{}); break;
-      case 2: f(N, std::integral_constant<int, 2>{}); break;
-      case 4: f(N, std::integral_constant<int, 4>{}); break;
-      case 6: f(N, std::integral_constant<int, 6>{}); break;
-      case 8: f(N, std::integral_constant<int, 8>{}); break;
-      default: f(N, std::integral_constant<int, 0>{}); break;
+      case 1: f(L, N, std::integral_constant<int, 1>{}); break;
+      case 2: f(L, N, std::integral_constant<int, 2>{}); break;
+      case 4: f(L, N, std::integral_constant<int, 4>{}); break;
+      case 6: f(L, N, std::integral_constant<int, 6>{}); break;
+      case 8: f(L, N, std::integral_constant<int, 8>{}); break;
+      default: f(L, N, std::integral_constant<int, 0>{}); break;
     }
   });
+}
+
+// Blocks covering T tokens.
+int token_blocks(int64_t T, int64_t E, bool wave_token = false) {
+  const int64_t tpb = wave_token ? kRouterWaves : tokens_per_block(E);
+  return static_cast<int>((T + tpb - 1) / tpb);
 }
 
 int check_router(int64_t T, int64_t E, int64_t k) {
@@ -525,9 +599,10 @@ extern "C" int moe_router_topk_fwd(const float* logits, float* scores, int64_t* 
   if (rc) return rc;
   MOE_REQUIRE(logits && scores && indices, MOE_ERR_INVALID, "router topk: null pointer");
   if (T == 0) return MOE_OK;
-  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((router_topk_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+  int blocks = token_blocks(T, E);
+  with_npl_k(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_fwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, scores, indices, static_cast<int>(T),
                        static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0);
   });
@@ -541,9 +616,10 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
   if (rc) return rc;
   MOE_REQUIRE(logits && indices && d_scores && d_logits, MOE_ERR_INVALID, "router topk bwd: null pointer");
   if (T == 0) return MOE_OK;
-  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+  int blocks = token_blocks(T, E, true);
+  with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
                        accumulate ? d_logits : nullptr, d_logits, static_cast<bf16_t*>(d_logits_bf16));
@@ -558,9 +634,10 @@ extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indi
   if (rc) return rc;
   MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "router topk bwd bf16: null pointer");
   if (T == 0) return MOE_OK;
-  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+  int blocks = token_blocks(T, E, true);
+  with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
                        d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16));
@@ -570,7 +647,7 @@ extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indi
 
 extern "C" size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E) {
   if (T < 0 || E < 1) return 0;
-  return static_cast<size_t>(aux_blocks(T) + kAuxGroups) * static_cast<size_t>(2 * E + 1) * sizeof(float);
+  return static_cast<size_t>(aux_blocks(T, E) + kAuxGroups) * static_cast<size_t>(2 * E + 1) * sizeof(float);
 }
 
 extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, int64_t T, int64_t E, int64_t k,
@@ -581,10 +658,11 @@ extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, 
   MOE_REQUIRE(T >= 1, MOE_ERR_INVALID, "aux loss: needs at least one token");
   MOE_REQUIRE(workspace_bytes >= moe_aux_loss_workspace_bytes(T, E), MOE_ERR_WORKSPACE,
               "aux loss: workspace %zu < %zu bytes", workspace_bytes, moe_aux_loss_workspace_bytes(T, E));
-  const int nblk = aux_blocks(T);
+  const int nblk = aux_blocks(T, E);
   float* ws = static_cast<float*>(workspace);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((aux_partial_kernel<decltype(N)::value, decltype(K)::value>), dim3(nblk),
+  with_npl_k(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((aux_partial_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(nblk),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, token_weight, static_cast<int>(T),
                        static_cast<int>(E), static_cast<int>(k), ws);
   });
@@ -607,10 +685,10 @@ extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, 
   if (rc) return rc;
   MOE_REQUIRE(logits && stats && d_aux && d_logits, MOE_ERR_INVALID, "aux loss bwd: null pointer");
   if (T == 0) return MOE_OK;
-  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl(E, [&](auto N) {
-    hipLaunchKernelGGL((aux_bwd_kernel<decltype(N)::value>), dim3(blocks), dim3(kRouterWaves * kWave), 0,
-                       as_stream(stream), logits, token_weight, stats, d_aux, static_cast<int>(T),
+  int blocks = token_blocks(T, E, true);
+  with_npl<true>(E, [&](auto L, auto N) {
+    hipLaunchKernelGGL((aux_bwd_kernel<decltype(L)::value, decltype(N)::value>), dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, token_weight, stats, d_aux, static_cast<int>(T),
                        static_cast<int>(E), d_logits, accumulate ? 1 : 0);
   });
   return launch_status("moe_aux_loss_bwd");
@@ -661,9 +739,10 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
   rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
                               static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
   if (rc) return rc;
-  int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+  int blocks = token_blocks(T, E);
+  with_npl_k(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
                        nullptr, nullptr);
@@ -673,7 +752,7 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
 
 extern "C" size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
   if (T < 0 || H < 1 || E < 1) return 0;
-  const int64_t blocks = (T + kRouterWaves - 1) / kRouterWaves;
+  const int64_t blocks = token_blocks(T, E);
   const size_t aux = static_cast<size_t>(blocks + kAuxGroups) * static_cast<size_t>(2 * E + 1) * sizeof(float);
   return moe_router_fwd_workspace_bytes(T, H, E) + aux;
 }
@@ -701,9 +780,10 @@ extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* lo
   rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
                               static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
   if (rc) return rc;
-  const int blocks = static_cast<int>((T + kRouterWaves - 1) / kRouterWaves);
-  with_npl_k(E, k, [&](auto N, auto K) {
-    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+  const int blocks = token_blocks(T, E);
+  with_npl_k(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
                        token_weight, aux_ws);

@@ -44,9 +44,12 @@ def test_library_exports_every_declared_symbol():
 def test_library_size_queries_and_argument_checks_run_without_a_gpu():
     lib = _lib.load()
     assert lib.moe_permute_workspace_bytes(32768, 128) == 16 * 129 * 4
-    # one partial row per 4-token block (at most 1024) plus 16 row-group sums, each 2E+1 floats
-    assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (1024 + 16) * 257 * 4
-    assert lib.moe_aux_loss_workspace_bytes(40, 8) == (10 + 16) * 17 * 4
+    # one partial row per block (16 tokens for E <= 256, else 4; at most 1024 rows)
+    # plus 16 row-group sums, each 2E+1 floats
+    assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (256 + 16) * 257 * 4
+    assert lib.moe_aux_loss_workspace_bytes(40, 8) == (3 + 16) * 17 * 4
+    assert lib.moe_aux_loss_workspace_bytes(4096, 512) == (1024 + 16) * 1025 * 4
+    assert lib.moe_aux_loss_workspace_bytes(1 << 20, 128) == (1024 + 16) * 257 * 4
     assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) >= 4096 * 128 * 4
     # invalid sizes are rejected before any HIP call
     rc = lib.moe_grouped_gemm_fwd(None, None, None, 1, 8, 8, 8, None, None)
