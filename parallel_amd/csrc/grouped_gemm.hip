@@ -190,12 +190,13 @@ __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t of
 // device from `offs` (the grid is sized without a host sync).
 //
 // Each block runs one continuous stream of k-steps over all its tiles: a DMA
-// cursor fills the LDS ring STAGES-1 k-steps ahead of the compute cursor and
-// runs straight across tile boundaries, so the ring never drains between
-// tiles.  When the compute cursor finishes a tile, the wave writes it out
-// (epilogue) while the DMA of the next tile is already in flight; the tile
-// wait of the following STAGES-1 steps leaves that epilogue's stores
-// outstanding, so they drain in the background.  Every epilogue issues the
+// cursor fills the LDS ring LEAD k-steps ahead of the compute cursor (3 of 5
+// stages with a block barrier every second k-step, else STAGES-1 with one per
+// k-step) and runs straight across tile boundaries, so the ring never drains
+// between tiles.  When the compute cursor finishes a tile, the wave writes it
+// out (epilogue) while the DMA of the next tile is already in flight; the
+// tile waits that follow leave that epilogue's stores outstanding, so they
+// drain in the background.  Every epilogue issues the
 // same number of store instructions per wave (out-of-range stores go to an
 // offset past the buffer resource and are dropped), which keeps those waits
 // exact.
@@ -252,7 +253,16 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
   constexpr int LPW_A = NI_A / NWAVES, LPW_B = NI_B / NWAVES;  // ... per wave and operand
   constexpr int LPW = LPW_A + LPW_B;
-  constexpr int WAIT = (STAGES - 2) * LPW;                     // DMA younger than the k-tile waited for
+  // Barrier cadence.  With a 5-deep ring the DMA runs LEAD = 3 k-steps ahead
+  // and the block synchronises on even k-steps only: an even step waits for
+  // its own k-tile and the next one, and the DMA of any step targets the
+  // stage read three steps earlier, which every wave had left by the last
+  // barrier.  Shallower rings synchronise every step with the DMA
+  // STAGES - 1 steps ahead.
+  constexpr bool PAIR = STAGES == 5;
+  constexpr int LEAD = PAIR ? STAGES - 2 : STAGES - 1;
+  constexpr int WAIT = PAIR ? LPW : (STAGES - 2) * LPW;        // DMA younger than the k-tiles waited for
+  constexpr int RELAX = PAIR ? 2 : STAGES - 1;                 // waits that an epilogue's stores precede
   constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
   constexpr int SLOT = 32 * WTN * 2;                           // staging bytes per wave (one 32-row pass)
   static_assert(BK == 32 || BK == 64, "swizzles and DMA mapping cover 32- and 64-deep k-tiles");
@@ -644,11 +654,11 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // wcol0 + j*32 + 8*q + 4*khalf + {0..3} holding acc[i][j][4q..4q+3].
   // This wave's staging slot (no other wave touches it) in the ring stage
   // that the compute cursor has just finished: no DMA targets that stage
-  // until the next k-step's barrier, and a barrier before the epilogue
+  // before the next block barrier, and a barrier before the epilogue
   // retires every wave's fragment reads of it.  Tiles written out before the
   // stream starts (empty weight-gradient groups) use the last stage, which
-  // the prologue DMA into stages 0 .. STAGES-2 leaves alone and the first
-  // k-step fills only after its barrier.
+  // the prologue DMA leaves alone and no k-step fills before the first
+  // barrier.
   char* slot = ring + (STAGES - 1) * STAGE_BYTES + wave * SLOT;
   auto swap_halves = [](uint4 v) { return make_uint4(v.z, v.w, v.x, v.y); };
   auto to_f32x8 = [](uint4 v, float* f) {
@@ -820,7 +830,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       if constexpr (MODE == MODE_KG) {  // (MG tiles always have k-steps)
         if (!p.accumulate) {
           epilogue(ct);
-          relax = STAGES - 1;
+          relax = RELAX;
         }
       }
     }
@@ -846,21 +856,26 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // wait already covers them.
   relax = 0;
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) dma_issue(s);
-  int cstage = 0, dstage = STAGES - 1;
+  for (int s = 0; s < LEAD; ++s) dma_issue(s);
+  int cstage = 0, dstage = LEAD;
+  int parity = 0;  // k-step count of the stream, mod 2
   if (any) {
     for (;;) {
-      // k-tile of this step landed: this wave's DMA (all but the WAIT younger
-      // instructions, plus the last epilogue's stores while they drain), then
-      // every wave's, via the barrier; the barrier also retires the reads of
-      // the stage the next DMA overwrites.
-      if (relax > 0) {
-        wait_vmcnt<WAIT + NST>();
-        --relax;
-      } else {
-        wait_vmcnt<WAIT>();
+      // k-tiles of this step (and, pairwise, the next) landed: this wave's
+      // DMA (all but the WAIT younger instructions, plus the last epilogue's
+      // stores while they drain), then every wave's, via the barrier; the
+      // barrier also retires the reads of the stages the next DMA overwrites.
+      const bool drain = relax > 0;
+      if (relax > 0) --relax;
+      if (!PAIR || parity == 0) {
+        if (drain) {
+          wait_vmcnt<WAIT + NST>();
+        } else {
+          wait_vmcnt<WAIT>();
+        }
+        barrier();
       }
-      barrier();
+      parity ^= 1;
       dma_prepare(dstage);
       if (n_act > 0) {
         // Issue priority while the wave feeds its MFMAs, so that on a shared
@@ -880,7 +895,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         slot = ring + (cstage == 0 ? STAGES - 1 : cstage - 1) * STAGE_BYTES + wave * SLOT;
         barrier();
         epilogue(ct);
-        relax = STAGES - 1;
+        relax = RELAX;
         if (!compute_seek(cj + 1)) break;
       }
     }
