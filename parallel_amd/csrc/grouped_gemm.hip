@@ -10,10 +10,10 @@
 // Tiling: WM x WN waves; each wave owns (BM/WM) x (BN/WN) of 32x32 MFMA
 // sub-tiles (v_mfma_f32_32x32x16_bf16, fp32 accumulators), its row sub-tiles
 // interleaved with the other wave rows'.  The expert GEMMs use 256x256 tiles
-// (512x128 when the output is at most 1024 columns wide) on 8 waves (two waves
+// (384x128 when the output is at most 1024 columns wide) on 8 waves (two waves
 // per SIMD, one workgroup per CU); the small router GEMMs use 128x128 on 4
 // waves.  Operands move from HBM to LDS by DMA (buffer_load_dwordx4 ... lds,
-// no register staging) into a 4- or 5-deep ring of 32-deep k-tiles that fills
+// no register staging) into a 5-deep ring of 32-deep k-tiles that fills
 // the 160 KiB of LDS, so three or four k-tiles of loads are in flight while
 // one is multiplied; each wave fires its share of a k-tile's DMA between its
 // MFMA groups.  At the roughly 256 rows per expert of a training step the
@@ -116,10 +116,10 @@ struct TileCfg {
 };
 // Expert GEMMs and weight gradients: 160 KiB ring, 8 waves.
 using BigTile = TileCfg<256, 256, 32, 2, 4, 5>;
-// Expert GEMMs with narrow outputs: 512-row tiles, so that an expert of up to
-// 512 rows is one m-tile and its weights stream through LDS once per n-tile;
-// 160 KiB ring, 8 waves.
-using TallTile = TileCfg<512, 128, 32, 4, 2, 4>;
+// Expert GEMMs with narrow outputs: 384-row tiles, so that an expert of up to
+// 384 rows is one m-tile and its weights stream through LDS once per n-tile;
+// 160 KiB ring (5 x 32 KiB, so the block barrier pairs k-steps), 8 waves.
+using TallTile = TileCfg<384, 128, 32, 4, 2, 5>;
 // Router GEMMs (N = E = 128): 80 KiB ring, 4 waves (two workgroups per CU).
 using SmallTile = TileCfg<128, 128, 32, 2, 2, 5>;
 
@@ -976,8 +976,8 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
 // Expert GEMM over grouped rows.  256x256 tiles do the most MFMA work per
 // k-step of LDS traffic, but with few output columns their grid (about one
 // or two m-tiles per expert times the column tiles) ends in a poorly
-// balanced last round; 512x128 tiles give one m-tile per expert and twice
-// the column tiles.
+// balanced last round; 384x128 tiles give one m-tile per expert of up to 384
+// rows and twice the column tiles.
 template <bool B_KCONTIG, int EPI>
 int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   const int out_cols = (EPI == EPI_SWIGLU_FWD) ? 2 * p.swiglu_I : p.N;
