@@ -245,7 +245,73 @@ def profile_summary(args) -> int:
         ]
         (prof / f"{tag}_{w.name}_pmc.txt").write_text("\n".join(body) + "\n")
     log(f"wrote {len(by_tag)} traffic summaries and kernel_stats_{w.name}.txt under {prof}")
+    if args.pmc_util and args.pmc_ta and args.pmc_tcp:
+        units_summary(args, w, prof, cmd)
     return 0
+
+
+_UNIT_COUNTERS = {
+    "pmc_util": "MfmaUtil LdsUtil LdsBankConflict",
+    "pmc_ta": "TA_BUSY_avr TA_ADDR_STALLED_BY_TC_CYCLES_sum GRBM_GUI_ACTIVE SQ_VMEM_TA_ADDR_FIFO_FULL "
+              "SQ_VMEM_TA_CMD_FIFO_FULL SQ_LDS_DATA_FIFO_FULL SQ_BUSY_CYCLES",
+    "pmc_tcp": "TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum TCP_PENDING_STALL_CYCLES_sum "
+               "TCP_TCR_TCP_STALL_CYCLES_sum GRBM_GUI_ACTIVE",
+}
+
+
+def units_summary(args, w, prof, cmd) -> None:
+    """The expert GEMMs' unit utilisation from three counter passes over this
+    script (--pmc-util, --pmc-ta, --pmc-tcp; one counter set per pass).
+    GRBM_GUI_ACTIVE sums the 8 XCDs, the SQ and TCP sums cover every CU, and
+    TA_BUSY_avr averages over the texture units."""
+    from collections import defaultdict
+
+    gemms = ["up_fwd", "down_fwd", "down_dgrad", "up_dgrad", "up_wgrad", "down_wgrad"]
+    acc = defaultdict(lambda: defaultdict(list))
+    for d in (args.pmc_util, args.pmc_ta, args.pmc_tcp):
+        per = defaultdict(dict)
+        for r in _read_csvs(d):
+            e = per[int(r["Dispatch_Id"])]
+            e["name"] = r["Kernel_Name"]
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        ids = sorted(per)
+        for i, tag in zip(ids, tag_dispatches([per[i]["name"] for i in ids])):
+            if tag in gemms and "grouped_gemm_kernel" in per[i]["name"]:  # not the SwiGLU backward
+                for c, v in per[i].items():
+                    if c != "name":
+                        acc[tag][c].append(v)
+    cus = 256
+    mean = statistics.fmean
+    rows = ["| GEMM | launches | MFMA busy | LDS active | TA busy | TA FIFO full | L1 waiting on L2 | L2 read latency |",
+            "|---|---|---|---|---|---|---|---|"]
+    for tag in gemms:
+        d = acc[tag]
+        if not d:
+            continue
+        cyc = mean(d["GRBM_GUI_ACTIVE"]) / 8.0  # per-XCD cycles
+        lat = sum(d["TCP_TCC_READ_REQ_LATENCY_sum"]) / sum(d["TCP_TCC_READ_REQ_sum"])
+        rows.append(f"| {tag} | {len(d['MfmaUtil'])} | {mean(d['MfmaUtil']):.0f}% | {mean(d['LdsUtil']):.0f}% | "
+                    f"{100 * mean(d['TA_BUSY_avr']) / cyc:.0f}% | "
+                    f"{100 * mean(d['SQ_VMEM_TA_ADDR_FIFO_FULL']) / (cus * cyc):.0f}% | "
+                    f"{100 * mean(d['TCP_PENDING_STALL_CYCLES_sum']) / (cus * cyc):.0f}% | {lat:.0f} cycles |")
+    conflicts = [mean(acc[t]["LdsBankConflict"]) for t in gemms if acc[t]]
+    body = [
+        f"# Expert-GEMM unit utilisation, workload {w.name} (per launch, averaged over the launches of each",
+        "# entry point in the profiled run: warm-up, instrumented and timed steps)",
+        "# commands (one counter set per pass):",
+        *[f"#   cd /tmp && rocprofv3 --pmc {c} -f csv -d <out>/{n} -o run -- python3 <repo>/bench.py --steps 2 "
+          f"--warmup 1 --no-cpu-baseline" for n, c in _UNIT_COUNTERS.items()],
+        *[f"#   {c}" for c in cmd.splitlines() if "--profile-summary" in c],
+        "# Normalisation: GRBM_GUI_ACTIVE sums the 8 XCDs (per-XCD cycles = value / 8; with the kernel",
+        "# durations this gives about 2.1 GHz); SQ_VMEM_TA_ADDR_FIFO_FULL and the TCP sums cover 256 CUs;",
+        "# TA_BUSY_avr is the average over the texture units. MfmaUtil and LdsUtil are rocprofv3's derived",
+        f"# metrics (busy cycles over active cycles x SIMDs / CUs). LdsBankConflict: "
+        f"{min(conflicts):.1f}-{max(conflicts):.1f}%.",
+        "# The weight-gradient GEMMs share one kernel; dispatches alternate up_wgrad, down_wgrad in each step.",
+        *rows,
+    ]
+    (prof / f"gemm_units_{w.name}_pmc.txt").write_text("\n".join(body) + "\n")
+    log(f"wrote gemm_units_{w.name}_pmc.txt")
 
 
 def cpu_baseline(w, tokens: int):
@@ -299,6 +365,9 @@ def main() -> int:
                     help="entry-point calls in the --pmc runs: warm-up + instrumented + timed steps (1 + 3 + 2)")
     ap.add_argument("--steps-profiled", type=int, default=10)
     ap.add_argument("--profile-commands", help="the rocprofv3 command lines, one per line, recorded in the summaries")
+    ap.add_argument("--pmc-util", help="counter_collection dir of a --pmc MfmaUtil LdsUtil LdsBankConflict run")
+    ap.add_argument("--pmc-ta", help="counter_collection dir of the texture-unit counter run")
+    ap.add_argument("--pmc-tcp", help="counter_collection dir of the L1 (TCP) counter run")
     args = ap.parse_args()
     if args.profile_summary:
         sys.path.insert(0, str(ROOT))
