@@ -985,8 +985,11 @@ int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   return launch<MODE_MG, B_KCONTIG, EPI, BigTile>(p, stream, name);
 }
 
-int check_common(const void* a, const void* b, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K) {
-  MOE_REQUIRE(a && b, MOE_ERR_INVALID, "grouped gemm: null operand");
+// Operand checks.  `a` holds M rows, as does `b` when b_rows (the weight
+// gradient's second operand); an operand of zero rows may be NULL.
+int check_common(const void* a, const void* b, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K,
+                 bool b_rows = false) {
+  MOE_REQUIRE((a || M == 0) && (b || (b_rows && M == 0)), MOE_ERR_INVALID, "grouped gemm: null operand");
   MOE_REQUIRE(G >= 1 && G <= 4096, MOE_ERR_UNSUPPORTED, "grouped gemm: G=%lld outside [1,4096]", (long long)G);
   MOE_REQUIRE(offs || G == 1, MOE_ERR_INVALID, "grouped gemm: offs may be NULL only for G == 1");
   MOE_REQUIRE(M >= 0 && N > 0 && K > 0, MOE_ERR_INVALID, "grouped gemm: bad sizes M=%lld N=%lld K=%lld",
@@ -1114,8 +1117,8 @@ extern "C" int moe_grouped_gemm_swiglu_fwd(const void* xp, const void* w_gate_up
                                            int64_t M, int64_t H, int64_t I, void* act, void* pre, void* stream) {
   int rc = check_common(xp, w_gate_up, offs, G, M, 2 * I, H);
   if (rc) return rc;
+  if (M == 0) return MOE_OK;  // no rows: empty outputs may be NULL
   MOE_REQUIRE(act && aligned16(act) && (!pre || aligned16(pre)), MOE_ERR_INVALID, "swiglu fwd: bad output pointer");
-  if (M == 0) return MOE_OK;
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(xp);
   p.B = static_cast<const bf16_t*>(w_gate_up);
@@ -1142,8 +1145,8 @@ extern "C" int moe_grouped_gemm_fwd(const void* a, const void* w, const int32_t*
                                     int64_t K, void* c, void* stream) {
   int rc = check_common(a, w, offs, G, M, N, K);
   if (rc) return rc;
-  MOE_REQUIRE(c && aligned16(c), MOE_ERR_INVALID, "grouped gemm fwd: bad output pointer");
   if (M == 0) return MOE_OK;
+  MOE_REQUIRE(c && aligned16(c), MOE_ERR_INVALID, "grouped gemm fwd: bad output pointer");
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(a);
   p.B = static_cast<const bf16_t*>(w);
@@ -1166,8 +1169,8 @@ extern "C" int moe_router_logits_fwd(const void* x, const void* wr, float* logit
                                      void* stream) {
   int rc = check_common(x, wr, nullptr, 1, T, E, H);
   if (rc) return rc;
-  MOE_REQUIRE(logits && aligned16(logits), MOE_ERR_INVALID, "router logits: bad output pointer");
   if (T == 0) return MOE_OK;
+  MOE_REQUIRE(logits && aligned16(logits), MOE_ERR_INVALID, "router logits: bad output pointer");
   return router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), logits,
                                 static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), 1,
                                 static_cast<int>(H), as_stream(stream));
@@ -1178,8 +1181,8 @@ extern "C" int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32
   // da[M,K] = dc[M,N] . w[g] (w [G,N,K]): GEMM-internal reduction over N, output width K.
   int rc = check_common(dc, w, offs, G, M, K, N);
   if (rc) return rc;
-  MOE_REQUIRE(da && aligned16(da), MOE_ERR_INVALID, "grouped gemm dgrad: bad output pointer");
   if (M == 0) return MOE_OK;
+  MOE_REQUIRE(da && aligned16(da), MOE_ERR_INVALID, "grouped gemm dgrad: bad output pointer");
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(dc);
   p.B = static_cast<const bf16_t*>(w);
@@ -1204,10 +1207,10 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   // d_pre, then the SwiGLU backward in place.
   int rc = check_common(dy, w_down, offs, G, M, I, H);
   if (rc) return rc;
+  if (M == 0) return MOE_OK;
   MOE_REQUIRE(pre && d_pre && aligned16(pre) && aligned16(d_pre), MOE_ERR_INVALID,
               "dgrad swiglu: bad pre/d_pre pointer");
   MOE_REQUIRE(M * I / 8 < (1ll << 31), MOE_ERR_UNSUPPORTED, "dgrad swiglu: too many rows");
-  if (M == 0) return MOE_OK;
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(dy);
   p.B = static_cast<const bf16_t*>(w_down);
@@ -1235,9 +1238,11 @@ namespace {
 int wgrad(const void* dc, const void* a, const int32_t* offs, int64_t G, int64_t M, int64_t N, int64_t K, void* dw,
           int dw_is_f32, int accumulate, int64_t bucket_rows, int64_t bucket_stride, void* stream, const char* name) {
   // dw[g][N,K] = dc[rows g, N]^T . a[rows g, K]: GEMM-internal output N x K, reduction over rows.
-  int rc = check_common(dc, a, offs, G, M, N, K);
+  // With no rows at all dW is still written (zeros) or left as it is (accumulate).
+  int rc = check_common(dc, a, offs, G, M, N, K, /*b_rows=*/true);
   if (rc) return rc;
   MOE_REQUIRE(dw && aligned16(dw), MOE_ERR_INVALID, "%s: bad output pointer", name);
+  if (M == 0) dc = a = dw;  // zero-byte operand resources: never read, but on a valid base
   GemmParams p{};
   p.A = static_cast<const bf16_t*>(dc);
   p.B = static_cast<const bf16_t*>(a);

@@ -9,6 +9,7 @@
 // Reference arithmetic: TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267
 // (router) and :514-593 (load_balancing_loss_func); the one-rank SP variant is
 // parallel/parallel/engine/model_parallel/sequence_parallel.py:239-280.
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm.h"
@@ -597,8 +598,8 @@ extern "C" int moe_router_topk_fwd(const float* logits, float* scores, int64_t* 
                                    int64_t k, int norm_topk_prob, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
+  if (T == 0) return MOE_OK;  // no tokens: empty buffers may be NULL
   MOE_REQUIRE(logits && scores && indices, MOE_ERR_INVALID, "router topk: null pointer");
-  if (T == 0) return MOE_OK;
   int blocks = token_blocks(T, E);
   with_npl_k(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_topk_fwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
@@ -614,8 +615,8 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
                                    void* d_logits_bf16, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
-  MOE_REQUIRE(logits && indices && d_scores && d_logits, MOE_ERR_INVALID, "router topk bwd: null pointer");
   if (T == 0) return MOE_OK;
+  MOE_REQUIRE(logits && indices && d_scores && d_logits, MOE_ERR_INVALID, "router topk bwd: null pointer");
   int blocks = token_blocks(T, E, true);
   with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
@@ -632,8 +633,8 @@ extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indi
                                         void* d_logits_bf16, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
-  MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "router topk bwd bf16: null pointer");
   if (T == 0) return MOE_OK;
+  MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "router topk bwd bf16: null pointer");
   int blocks = token_blocks(T, E, true);
   with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
@@ -683,8 +684,8 @@ extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, 
                                 int64_t T, int64_t E, float* d_logits, int accumulate, void* stream) {
   int rc = check_router(T, E, 1);
   if (rc) return rc;
-  MOE_REQUIRE(logits && stats && d_aux && d_logits, MOE_ERR_INVALID, "aux loss bwd: null pointer");
   if (T == 0) return MOE_OK;
+  MOE_REQUIRE(logits && stats && d_aux && d_logits, MOE_ERR_INVALID, "aux loss bwd: null pointer");
   int blocks = token_blocks(T, E, true);
   with_npl<true>(E, [&](auto L, auto N) {
     hipLaunchKernelGGL((aux_bwd_kernel<decltype(L)::value, decltype(N)::value>), dim3(blocks),
@@ -702,7 +703,7 @@ void router_split(int64_t T, int64_t H, int64_t E, int& splits, int& k_chunk) {
   // cover the CUs more evenly but write and re-read more fp32 partials: at
   // T = 4096, E = 128 the GEMM plus the reduction took 34 us with 16 splits,
   // 29 us with 8 and 28 us with 4.
-  int64_t tiles = ((T + 127) / 128) * ((E + 127) / 128);
+  const int64_t tiles = std::max<int64_t>(1, ((T + 127) / 128) * ((E + 127) / 128));  // T = 0: no tiles
   int64_t want = (256 + tiles - 1) / tiles;
   int64_t max_splits = (H + 63) / 64;
   if (want > max_splits) want = max_splits;
@@ -724,11 +725,11 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
                               void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
-  MOE_REQUIRE(x && wr && logits && scores && indices, MOE_ERR_INVALID, "router fwd: null pointer");
+  MOE_REQUIRE(wr && (T == 0 || (x && logits && scores && indices)), MOE_ERR_INVALID, "router fwd: null pointer");
   MOE_REQUIRE(H > 0 && H % 8 == 0 && E % 8 == 0 && aligned16(x) && aligned16(wr), MOE_ERR_UNSUPPORTED,
               "router fwd: H (%lld) and E (%lld) must be multiples of 8 with 16-byte aligned operands",
               (long long)H, (long long)E);
-  if (T == 0) return MOE_OK;
+  if (T == 0) return MOE_OK;  // no tokens: empty buffers may be NULL
   const size_t need = moe_router_fwd_workspace_bytes(T, H, E);
   MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "router fwd: workspace %zu < %zu bytes",
               workspace_bytes, need);
@@ -809,7 +810,9 @@ extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, in
 extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, const void* wr, void* dx, void* dwr,
                                      int64_t T, int64_t H, int64_t E, void* workspace, size_t workspace_bytes,
                                      void* stream) {
-  MOE_REQUIRE(d_logits_bf16 && x && wr && dx && dwr, MOE_ERR_INVALID, "router logits bwd: null pointer");
+  // With no tokens only dWr (zeros) is written; the empty buffers may be NULL.
+  MOE_REQUIRE(wr && dwr && (T == 0 || (d_logits_bf16 && x && dx)), MOE_ERR_INVALID,
+              "router logits bwd: null pointer");
   MOE_REQUIRE(T >= 0 && H > 0 && E > 0 && H % 8 == 0 && E % 8 == 0, MOE_ERR_UNSUPPORTED,
               "router logits bwd: H (%lld) and E (%lld) must be multiples of 8", (long long)H, (long long)E);
   MOE_REQUIRE(aligned16(dwr), MOE_ERR_INVALID, "router logits bwd: dwr must be 16-byte aligned");

@@ -238,3 +238,25 @@ def test_experts_concentrated_routing():
         close_bf16(a.grad, b.grad, f"concentrated {name}")
     unused = [e for e in range(E) if e not in (3, 7, 8, 15)]
     assert not dl[2].grad[unused].any() and not dl[3].grad[unused].any(), "experts without routes get zero dW"
+
+
+def test_empty_batch_through_router_and_experts():
+    """A batch with no tokens (an EP rank can receive no rows): the reference's
+    grouped experts return [0, H] and every weight gradient is zero.  Every
+    entry point on the path sees size 0 with NULL pointers for the empty
+    buffers."""
+    H, E, k, I = 256, 16, 4, 128
+    g = torch.Generator().manual_seed(22)
+    x = torch.empty(0, H, dtype=BF, device=DEV).requires_grad_()
+    rw = (torch.randn(E, H, generator=g) * 0.05).to(DEV, BF).requires_grad_()
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(DEV, BF).requires_grad_()
+    dn = (torch.randn(E, H, I, generator=g) * 0.05).to(DEV, BF).requires_grad_()
+    logits, scores, idx = ops.router_fwd(x, rw, k, True)
+    assert logits.shape == (0, E) and scores.shape == (0, k) and idx.shape == (0, k)
+    out = ops.experts(x, idx, scores, gu, dn)
+    assert out.shape == (0, H)
+    (out.float().sum() + scores.sum() + logits.sum()).backward()
+    torch.cuda.synchronize()
+    assert x.grad is not None and x.grad.shape == (0, H)
+    for name, p in (("router", rw), ("gate_up_proj", gu), ("down_proj", dn)):
+        assert p.grad is not None and p.grad.shape == p.shape and not p.grad.any(), f"{name}: dW must be zero"

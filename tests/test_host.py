@@ -141,3 +141,48 @@ def test_bench_tags_kernel_dispatches_by_entry_point():
         "down_dgrad", "down_dgrad", "up_dgrad", "permute_bwd", "up_wgrad", "down_wgrad",
         "router_gemm_bwd", "router_gemm_bwd",
     ]
+
+
+def test_size_queries_accept_empty_and_tiny_shapes():
+    """Every workspace query is host arithmetic only; with no tokens or one
+    token it must return (no division by a zero tile count) and never ask for
+    less than the non-empty case of the same layer."""
+    lib = _lib.load()
+    for T in (0, 1, 7):
+        for E in (1, 8, 128, 1024):
+            assert lib.moe_router_fwd_workspace_bytes(T, 2048, E) >= 0
+            assert lib.moe_router_aux_fwd_workspace_bytes(T, 2048, E) >= 0
+            assert lib.moe_router_logits_bwd_workspace_bytes(T, 2048, E) >= 0
+            assert lib.moe_aux_loss_workspace_bytes(T, E) >= 0
+            assert lib.moe_permute_workspace_bytes(T * 8, E) >= 0
+        assert lib.moe_rmsnorm_bwd_workspace_bytes(T, 2048) >= 0
+    assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) >= lib.moe_router_fwd_workspace_bytes(1, 2048, 128)
+
+
+def test_zero_size_calls_accept_null_buffers_without_a_gpu():
+    """With no rows or tokens every entry point whose work is empty returns 0
+    before any HIP call, with NULL for the empty buffers (an EP rank can
+    receive no rows).  The non-empty weight buffers are a host stand-in that
+    is never dereferenced."""
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(1 << 12)
+    b = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    E, H, I, k = 16, 256, 128, 4
+    calls = {
+        "swiglu_fwd": lambda: lib.moe_grouped_gemm_swiglu_fwd(None, b, b, E, 0, H, I, None, None, None),
+        "fwd": lambda: lib.moe_grouped_gemm_fwd(None, b, b, E, 0, H, I, None, None),
+        "dgrad": lambda: lib.moe_grouped_gemm_dgrad(None, b, b, E, 0, 2 * I, H, None, None),
+        "dgrad_swiglu": lambda: lib.moe_grouped_gemm_dgrad_swiglu_bwd(None, b, None, b, E, 0, H, I, None, None),
+        "router_fwd": lambda: lib.moe_router_fwd(None, b, None, None, None, None, 0, H, E, k, 1, b, 16, None),
+        "topk_fwd": lambda: lib.moe_router_topk_fwd(None, None, None, 0, E, k, 1, None),
+        "topk_bwd": lambda: lib.moe_router_topk_bwd(None, None, None, 0, E, k, 1, None, 0, None, None),
+        "topk_bwd_bf16": lambda: lib.moe_router_topk_bwd_bf16(None, None, None, None, 0, E, k, 1, None, None),
+        "combine_fwd": lambda: lib.moe_combine_fwd(None, None, None, E, None, 0, H, k, None, None),
+        "combine_bwd": lambda: lib.moe_combine_bwd(None, None, None, None, E, None, 0, H, k, None, None, None),
+        "permute_bwd": lambda: lib.moe_permute_bwd(None, None, None, E, 0, H, k, None, None, None),
+    }
+    for name, call in calls.items():
+        assert call() == _lib.MOE_OK, f"{name}: {lib.moe_last_error()}"
+    # a missing non-empty operand is still an error
+    assert lib.moe_grouped_gemm_fwd(None, None, b, E, 0, H, I, None, None) == _lib.MOE_ERR_INVALID
+    assert lib.moe_grouped_gemm_fwd(None, b, b, E, 8, H, I, None, None) == _lib.MOE_ERR_INVALID
