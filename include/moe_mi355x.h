@@ -10,7 +10,11 @@
  * Element types: "bf16" buffers hold IEEE bfloat16 as uint16; "f32" is IEEE
  * float; indices are int64 where the reference exposes torch.long tensors and
  * int32 for internal permutation maps.  Device pointers must be 16-byte
- * aligned and row strides (in elements) multiples of 8.
+ * aligned and row strides (in elements) multiples of 8.  A buffer of zero
+ * elements (no tokens or no routed rows, as on an EP rank that receives
+ * none) may be NULL; the entry point then does nothing, except that weight
+ * gradients are still written (zeros) or, when accumulating, left as they
+ * are.
  *
  * Return value: MOE_OK (0) or a negative MOE_ERR_* status; moe_last_error()
  * gives a message for the last failure on the calling thread.
