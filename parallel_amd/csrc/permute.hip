@@ -23,7 +23,7 @@
 
 namespace moe {
 
-constexpr int kChunk = 2048;       // slots per block in count/scatter
+constexpr int kChunk = 512;        // slots per block in count/scatter
 constexpr int kPermThreads = 256;  // 4 waves
 constexpr int kPerThread = kChunk / kPermThreads;
 constexpr int kMaxBuckets = 1024;  // real buckets; +1 for the sentinel bucket
@@ -68,9 +68,9 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
   const int nb1 = nb + 1;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wave = tid >> 6;
-  // Column prefix over blocks (per bucket), exclusive; 16 rows' loads in
+  // Column prefix over blocks (per bucket), exclusive; 32 rows' loads in
   // flight at a time.
-  constexpr int kRows = 16;
+  constexpr int kRows = 32;
   for (int e = tid; e < nb1; e += blockDim.x) {
     int run = 0;
     for (int b0 = 0; b0 < nblk; b0 += kRows) {

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_size_queries_and_argument_checks_run_without_a_gpu():
     lib = _lib.load()
-    assert lib.moe_permute_workspace_bytes(32768, 128) == 16 * 129 * 4
+    assert lib.moe_permute_workspace_bytes(32768, 128) == 64 * 129 * 4  # 512-route chunks x (E + sentinel)
     # one partial row per block (16 tokens for E <= 256, else 4; at most 1024 rows)
     # plus 16 row-group sums, each 2E+1 floats
     assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (256 + 16) * 257 * 4
