@@ -397,28 +397,50 @@ def main() -> int:
     from parallel_amd.workloads import WORKLOADS, make_block_inputs
 
     w = WORKLOADS[args.config]
-    if w.local_experts:
-        raise SystemExit(f"{args.config} is a parity configuration, not a bench line; use c2, c4 or c5")
     dev = "cuda"
     torch.manual_seed(0)
     inp = make_block_inputs(w, seed=0, device=dev, dtype=torch.bfloat16, weights_on_device_rng=True)
-    x = inp["x"].requires_grad_()
-    rw = inp["router_weight"].requires_grad_()
     gu = inp["gate_up_proj"].requires_grad_()
     dn = inp["down_proj"].requires_grad_()
-    d_out = inp["d_out"]
-    bias = inp.get("logit_bias")
-    coef = torch.tensor(w.aux_coef, device=dev)
-    params = (x, rw, gu, dn)
-    log(f"workload {w.name}: T={w.tokens} H={w.hidden} E={w.experts} k={w.top_k} I={w.intermediate}")
+    if w.local_experts:
+        # C3: the expert step of EP rank 0 on its receive buffer (source-rank
+        # major rows, one local expert each, token_dispatch.py:101-158), as a
+        # rank of an ep=2 group runs it between the two exchanges.
+        from parallel_amd.workloads import ep_receive_buffer
 
-    def step():
-        for p in params:
-            p.grad = None
-        logits, scores, idx = ops.router_fwd(x, rw, w.top_k, w.norm_topk_prob, bias)
-        out = ops.experts(x, idx, scores, gu, dn)
-        aux = load_balancing_loss_func((logits,), w.experts, w.top_k)
-        torch.autograd.backward([out, aux], [d_out, coef])
+        _, _, (src, tok, lexp, lsc) = ep_receive_buffer(w, seed=0)
+        rows = len(src)
+        g = torch.Generator(device=dev).manual_seed(1)
+        xs = torch.randn(w.sources, w.tokens, w.hidden, device=dev, generator=g).to(torch.bfloat16)
+        x = xs[torch.from_numpy(src).to(dev), torch.from_numpy(tok).to(dev)].contiguous().requires_grad_()
+        r_idx = torch.from_numpy(lexp).view(rows, 1).to(dev)
+        r_sc = torch.from_numpy(lsc).view(rows, 1).to(dev).requires_grad_()
+        d_out = torch.randn(rows, w.hidden, device=dev, generator=g).to(torch.bfloat16)
+        params = (x, r_sc, gu, dn)
+        log(f"workload {w.name}: {w.sources} x {w.tokens} source tokens, {rows} routed rows to "
+            f"{w.local_experts} of {w.experts} experts, H={w.hidden} I={w.intermediate}")
+
+        def step():
+            for p in params:
+                p.grad = None
+            ops.experts(x, r_idx, r_sc, gu, dn).backward(d_out)
+    else:
+        rows = w.slots
+        x = inp["x"].requires_grad_()
+        rw = inp["router_weight"].requires_grad_()
+        d_out = inp["d_out"]
+        bias = inp.get("logit_bias")
+        coef = torch.tensor(w.aux_coef, device=dev)
+        params = (x, rw, gu, dn)
+        log(f"workload {w.name}: T={w.tokens} H={w.hidden} E={w.experts} k={w.top_k} I={w.intermediate}")
+
+        def step():
+            for p in params:
+                p.grad = None
+            logits, scores, idx = ops.router_fwd(x, rw, w.top_k, w.norm_topk_prob, bias)
+            out = ops.experts(x, idx, scores, gu, dn)
+            aux = load_balancing_loss_func((logits,), w.experts, w.top_k)
+            torch.autograd.backward([out, aux], [d_out, coef])
 
     for _ in range(args.warmup):
         step()
@@ -452,10 +474,15 @@ def main() -> int:
     _lib.TIMER.only = None
     dominant_ms = _lib.TIMER.durations_ms()[dominant]
     ms_per_step = 1e3 * elapsed / args.steps
-    tokens_per_s = w.tokens * args.steps / elapsed
+    tokens_per_s = w.sources * w.tokens * args.steps / elapsed  # source tokens (one source but for C3)
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:,.0f} tokens/s")
 
-    work = kernel_work(w, w.tokens, w.slots)
+    if w.local_experts:  # the experts see `rows` tokens of one route each, over the local experts
+        import dataclasses
+
+        work = kernel_work(dataclasses.replace(w, experts=w.local_experts, top_k=1), rows, rows)
+    else:
+        work = kernel_work(w, w.tokens, w.slots)
     kernels = {}
     for tag, ds in sorted(durations.items()):
         avg = statistics.fmean(ds)
@@ -489,10 +516,11 @@ def main() -> int:
         roofline["mfma_tflops"] = round(flops / avg_s / 1e12, 1)
     gemm_tags = [t for t in ("up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad") if t in durations]
     gemm_s = sum(statistics.fmean(durations[t]) for t in gemm_tags) * 1e-3
-    gemm_tflops = w.gemm_flops() / gemm_s / 1e12 if gemm_s else None
+    gemm_flops = w.gemm_flops(rows)  # fwd + bwd over the routed rows
+    gemm_tflops = gemm_flops / gemm_s / 1e12 if gemm_s else None
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not w.local_experts:
         log(f"cpu baseline: {args.cpu_baseline_tokens} tokens on {torch.get_num_threads()} threads")
         cpu = cpu_baseline(w, args.cpu_baseline_tokens)
         log(f"cpu baseline: {cpu['value']:,.0f} tokens/s")
@@ -513,7 +541,7 @@ def main() -> int:
         "config": {"workload": f"{w.name}: Qwen3-30B-A3B MoE block" if w.name in ("c2", "c4") else w.name,
                    "tokens": w.tokens, "hidden": w.hidden, "experts": w.experts, "top_k": w.top_k,
                    "moe_intermediate": w.intermediate, "router_logits": "fp32", "aux_coef": w.aux_coef},
-        "grouped_gemm": {"flops_fwd_bwd": w.gemm_flops(), "time_ms": round(gemm_s * 1e3, 4),
+        "grouped_gemm": {"flops_fwd_bwd": gemm_flops, "time_ms": round(gemm_s * 1e3, 4),
                          "tflops": round(gemm_tflops, 1) if gemm_tflops else None,
                          "mfma_frac": round(gemm_tflops / MFMA_BF16_PEAK_TFLOPS, 4) if gemm_tflops else None},
         "roofline": roofline,
@@ -521,6 +549,11 @@ def main() -> int:
         "kernels_source": f"untimed instrumented pass of {args.instrumented_steps} steps (events around every launch)",
         "cpu_baseline": cpu,
     }
+    if w.local_experts:
+        result["config"].update(sources=w.sources, local_experts=w.local_experts, routed_rows=rows,
+                                zipf_alpha=w.zipf_alpha)
+        result["routed_slots_per_s"] = round(rows * args.steps / elapsed, 1)
+        result["value_is"] = "source tokens/s (sources x tokens / step time); routed_slots_per_s is rows / step time"
     print(json.dumps(result), flush=True)
     return 0
 
