@@ -46,6 +46,10 @@ constexpr int kHalfMirror = 0x141;
 constexpr int kMirror = 0x140;
 constexpr int kBcast15 = 0x142;   // lane 15 of row r -> row r+1 (rows 1, 3 enabled)
 constexpr int kBcast31 = 0x143;   // lane 31 -> rows 2, 3
+constexpr int kRowShr1 = 0x111;   // row_shr:n = 0x110 + n, within 16-lane rows
+constexpr int kRowShr2 = 0x112;
+constexpr int kRowShr4 = 0x114;
+constexpr int kRowShr8 = 0x118;
 }  // namespace dpp
 
 template <int CTRL, int ROW_MASK = 0xF>
@@ -101,14 +105,19 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   i = __builtin_amdgcn_readlane(i, 63);
 }
 
-// Inclusive prefix sum across the wave (Hillis-Steele over 6 steps).
+// Inclusive prefix sum across the wave (every lane active): Hillis-Steele
+// within each 16-lane row by DPP row shifts (lanes shifted in from outside
+// the row add 0), then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15) and lane 31's into rows 2 and 3 (row_bcast:31).  DPP moves
+// take a few cycles each, against an LDS round trip per step for
+// ds_bpermute shuffles.
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    int n = __shfl_up(v, o, kWave);
-    if (lane >= o) v += n;
-  }
+  v += dpp_move_i<dpp::kRowShr1>(0, v);
+  v += dpp_move_i<dpp::kRowShr2>(0, v);
+  v += dpp_move_i<dpp::kRowShr4>(0, v);
+  v += dpp_move_i<dpp::kRowShr8>(0, v);
+  v += dpp_move_i<dpp::kBcast15, 0xA>(0, v);
+  v += dpp_move_i<dpp::kBcast31, 0xC>(0, v);
   return v;
 }
 

@@ -74,6 +74,10 @@ struct GemmParams {
   // elements into C instead of g * stride_cg.
   int bucket_rows;
   int64_t bucket_stride;
+  // KG with groups: split the tiles over the XCDs by cost (k-steps plus an
+  // epilogue allowance per tile) instead of by count (set by the host when
+  // the costs fit in 30 bits).
+  int cost_split;
 };
 
 // ---------------------------------------------------------------- helpers
@@ -106,6 +110,74 @@ __device__ __forceinline__ int count_tiles(const int32_t* offs, int G, int rows,
     total += __builtin_amdgcn_readlane(wave_inclusive_scan(nt), kWave - 1);
   }
   return __builtin_amdgcn_readfirstlane(total);
+}
+
+// Weight gradients (KG): a tile of group g costs its k-steps, ceil(rows_g /
+// BK), plus kEpiSteps for its epilogue.  Returns (split(part),
+// split(part + 1)), split(x) being the first tile, in group-major order, whose
+// cost start is at least x / kNumXcd of the total (wave-uniform): XCD x takes
+// tiles [split(x), split(x + 1)).  Under skewed routing the tiles of the
+// heavy experts are many times longer than the rest, and a split by count
+// leaves some XCDs long tails.  Returns (-1, -1) when the costs are near
+// uniform: the split by count is then as balanced and keeps whole rounds of
+// tiles per block.
+constexpr int kEpiSteps = 2;
+template <int BK>
+__device__ int2 kg_cost_split(const int32_t* offs, int G, int rows, int per_group, int part) {
+  const int lane = threadIdx.x & (kWave - 1);
+  auto tile_cost = [&](int g) {
+    if (g >= G) return 0;
+    const int hi = min(max(offs[g], 0), rows);
+    const int lo = g ? min(max(offs[g - 1], 0), hi) : 0;
+    return (hi - lo + BK - 1) / BK + kEpiSteps;
+  };
+  // Up to kCostChunks x 64 groups, every chunk's offsets are loaded at once
+  // (one memory round trip at kernel start instead of one per chunk).
+  constexpr int kCostChunks = 4;
+  const bool cached = G <= kCostChunks * kWave;
+  int tcr[kCostChunks];
+#pragma unroll
+  for (int c = 0; c < kCostChunks; ++c) tcr[c] = cached ? tile_cost(c * kWave + lane) : 0;
+  auto chunk_cost = [&](int c0) {
+    int v = 0;
+#pragma unroll
+    for (int c = 0; c < kCostChunks; ++c)
+      if (cached && c0 == c * kWave) v = tcr[c];
+    return cached ? v : tile_cost(c0 + lane);
+  };
+  int total = 0;
+  float mx = 0.0f;  // largest tile cost
+  for (int c0 = 0; c0 < G; c0 += kWave) {
+    const int tc = chunk_cost(c0);
+    total += __builtin_amdgcn_readlane(wave_inclusive_scan(per_group * tc), kWave - 1);
+    mx = fmaxf(mx, wave_max(static_cast<float>(tc)));
+  }
+  // Near-uniform costs (the largest within a quarter of the mean): the split
+  // by count is as balanced and keeps whole rounds of tiles per block.
+  if (4.0f * mx * static_cast<float>(G) * per_group <= 5.0f * static_cast<float>(total)) return make_int2(-1, -1);
+  // Both boundaries in one more pass (its loads hit the cache the first filled).
+  int t_lo = static_cast<int>(static_cast<int64_t>(total) * part / kNumXcd);
+  int t_hi = static_cast<int>(static_cast<int64_t>(total) * (part + 1) / kNumXcd);
+  int b_lo = part <= 0 ? 0 : -1, b_hi = part + 1 >= kNumXcd ? G * per_group : -1;
+  int base = 0;  // cost of the groups before this chunk
+  for (int c0 = 0; c0 < G && (b_lo < 0 || b_hi < 0); c0 += kWave) {
+    const int tc = chunk_cost(c0);
+    const int incl = wave_inclusive_scan(per_group * tc);
+    const int tot = __builtin_amdgcn_readlane(incl, kWave - 1);
+    auto locate = [&](int target) {
+      const int t = target - base;  // wave-uniform, and t < tot = incl[63]
+      const int q = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(incl > t)));  // first lane past t
+      const int before = __builtin_amdgcn_readlane(incl - per_group * tc, q);
+      const int cq = __builtin_amdgcn_readlane(tc, q);
+      return (c0 + q) * per_group + min((t - before + cq - 1) / cq, per_group);
+    };
+    if (b_lo < 0 && t_lo - base < tot) b_lo = locate(t_lo);
+    if (b_hi < 0 && t_hi - base < tot) b_hi = locate(t_hi);
+    base += tot;
+  }
+  if (b_lo < 0) b_lo = G * per_group;
+  if (b_hi < 0) b_hi = G * per_group;
+  return make_int2(__builtin_amdgcn_readfirstlane(b_lo), __builtin_amdgcn_readfirstlane(b_hi));
 }
 
 // Tile configurations: BK-deep k-tiles staged through a STAGES-deep LDS ring.
@@ -293,9 +365,18 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const int nbx = gridDim.x / kNumXcd;  // the grid is a multiple of kNumXcd
   const int xcd = blockIdx.x % kNumXcd, xidx = blockIdx.x / kNumXcd;
   const int real = (MODE == MODE_MG && p.offs) ? count_tiles<BM>(p.offs, p.G, p.rows, p.n_tiles) : p.total_tiles;
-  const int share = (real + kNumXcd - 1) / kNumXcd;
-  const int first = xcd * share;
-  const int span = min(share, real - first);
+  int first, span;
+  const int2 range = (MODE == MODE_KG && p.cost_split)
+                         ? kg_cost_split<BK>(p.offs, p.G, p.rows, p.n_tiles * p.m_tiles_max, xcd)
+                         : make_int2(-1, -1);
+  if (range.x >= 0) {
+    first = range.x;
+    span = range.y - range.x;
+  } else {
+    const int share = (real + kNumXcd - 1) / kNumXcd;
+    first = xcd * share;
+    span = min(share, real - first);
+  }
   const int ntiles = __builtin_amdgcn_readfirstlane(span > xidx ? (span - xidx + nbx - 1) / nbx : 0);
   if (ntiles <= 0) return;
 
@@ -953,6 +1034,11 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
   }
   if (tiles <= 0) return MOE_OK;
   MOE_REQUIRE(tiles < (1ll << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", name);
+  if (MODE == MODE_KG) {  // cost split when every group cost and their sum fit in 30 bits
+    const int64_t per_group = static_cast<int64_t>(p.n_tiles) * p.m_tiles_max;
+    const int64_t bound = per_group * (p.rows / CFG::BK + p.G * (1 + kEpiSteps));
+    p.cost_split = (p.offs && p.G > 1 && bound < (1ll << 30)) ? 1 : 0;
+  }
   p.total_tiles = static_cast<int>(tiles);
   // Persistent grid: as many blocks as fit at once (capped by the tile
   // count), a multiple of the XCD count.
