@@ -514,7 +514,8 @@ def main() -> int:
     roofline["flops_per_launch"] = flops
     if flops is not None:
         roofline["mfma_tflops"] = round(flops / avg_s / 1e12, 1)
-    gemm_tags = [t for t in ("up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad") if t in durations]
+    gemm_tags = [t for t in ("up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad")
+                 if t in durations]
     gemm_s = sum(statistics.fmean(durations[t]) for t in gemm_tags) * 1e-3
     gemm_flops = w.gemm_flops(rows)  # fwd + bwd over the routed rows
     gemm_tflops = gemm_flops / gemm_s / 1e12 if gemm_s else None

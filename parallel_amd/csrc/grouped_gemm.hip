@@ -762,11 +762,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
     // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
     const int esize = (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) ? 4 : 2;
-    const int64_t c_base = (MODE == MODE_KG) ? (p.bucket_rows ? static_cast<int64_t>(t.g / p.bucket_rows) * p.bucket_stride +
-                                                                 static_cast<int64_t>(t.g % p.bucket_rows) * p.stride_cg
-                                                               : static_cast<int64_t>(t.g) * p.stride_cg)
-                         : (EPI == EPI_F32)  ? static_cast<int64_t>(t.split) * p.split_stride
-                                             : 0;
+    const int64_t g_off = p.bucket_rows ? static_cast<int64_t>(t.g / p.bucket_rows) * p.bucket_stride +
+                                              static_cast<int64_t>(t.g % p.bucket_rows) * p.stride_cg
+                                        : static_cast<int64_t>(t.g) * p.stride_cg;
+    const int64_t c_base = (MODE == MODE_KG)  ? g_off
+                           : (EPI == EPI_F32) ? static_cast<int64_t>(t.split) * p.split_stride
+                                              : 0;
     const __amdgpu_buffer_rsrc_t rsC = make_rsrc(uniform_ptr(static_cast<char*>(p.C) + c_base * esize), p.c_bytes);
     if (EPI == EPI_F32 || (EPI == EPI_WGRAD && p.ldp)) {
       // fp32 outputs (split-K partials, fp32 weight gradients): direct 16-byte stores.

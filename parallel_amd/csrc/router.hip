@@ -689,8 +689,8 @@ extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, 
   int blocks = token_blocks(T, E, true);
   with_npl<true>(E, [&](auto L, auto N) {
     hipLaunchKernelGGL((aux_bwd_kernel<decltype(L)::value, decltype(N)::value>), dim3(blocks),
-                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, token_weight, stats, d_aux, static_cast<int>(T),
-                       static_cast<int>(E), d_logits, accumulate ? 1 : 0);
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, token_weight, stats, d_aux,
+                       static_cast<int>(T), static_cast<int>(E), d_logits, accumulate ? 1 : 0);
   });
   return launch_status("moe_aux_loss_bwd");
 }
