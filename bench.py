@@ -314,6 +314,20 @@ def units_summary(args, w, prof, cmd) -> None:
     log(f"wrote gemm_units_{w.name}_pmc.txt")
 
 
+def cpu_model_name() -> str | None:
+    """The host CPU's model name, as lscpu's "Model name" shows it (read from
+    /proc/cpuinfo, where lscpu takes it, so that no child process is started
+    from a process that holds the GPU)."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(w, tokens: int):
     """Reference op sequence on the host CPU (bounded sample of the same layer)."""
     import torch
@@ -335,6 +349,9 @@ def cpu_baseline(w, tokens: int):
         "value": round(tokens / med, 1),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model_name(),
+        "torch_threads": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{tokens} tokens of the {w.name} layer (H={w.hidden}, E={w.experts}, top-{w.top_k}, "
                   f"I={w.intermediate}), bf16, fwd+bwd via F.grouped_mm on the CPU; median of 3 after 1 warm-up "

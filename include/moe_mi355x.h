@@ -258,7 +258,9 @@ int moe_grouped_gemm_dgrad(const void* dc, const void* w, const int32_t* offs,
                            void* da, void* stream);
 
 /* d_act[M,I] = dy[M,H] · w_down[g] (w_down [G,H,I]) fused with the SwiGLU
- * backward against the saved pre[M,2I]: writes d_pre[M,2I] = (d_gate | d_up). */
+ * backward against the saved pre[M,2I]: writes d_pre[M,2I] = (d_gate | d_up)
+ * for the rows of the groups; rows at or beyond offs[G-1] are neither read
+ * nor written. */
 int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_down,
                                       const void* pre, const int32_t* offs,
                                       int64_t G, int64_t M, int64_t H,

@@ -81,15 +81,18 @@ def topk_softmax(logits: torch.Tensor, top_k: int, norm_topk_prob: bool):
 
 
 def topk_ties(logits: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-    """Tokens whose k-th and (k+1)-th probabilities are exactly equal (order unpinned)."""
+    """Tokens whose selected experts or their order depend on how torch.topk breaks
+    exact ties (unpinned): two equal probabilities among the first k+1 sorted
+    values, i.e. inside the top k (their order is ambiguous) or at the k-th /
+    (k+1)-th boundary (the selection is ambiguous).  With k == E there is no
+    boundary, but ties inside still make the order ambiguous."""
     probs = torch.softmax(logits.float(), dim=-1)
     k = indices.shape[1]
     srt = torch.sort(probs, dim=-1, descending=True).values
-    if k >= probs.shape[1]:
+    last = min(k, probs.shape[1] - 1)  # adjacent pairs (i, i+1) with i < last decide the top k
+    if last <= 0:
         return torch.zeros(probs.shape[0], dtype=torch.bool)
-    tied_boundary = srt[:, k - 1] == srt[:, k]
-    tied_inside = (srt[:, : k - 1] == srt[:, 1:k]).any(dim=1) if k > 1 else torch.zeros_like(tied_boundary)
-    return tied_boundary | tied_inside
+    return (srt[:, :last] == srt[:, 1:last + 1]).any(dim=1)
 
 
 # --------------------------------------------------------------- permutation

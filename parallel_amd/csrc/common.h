@@ -125,6 +125,20 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
 
+// Per-device launch facts (mutex-guarded, computed once per device).
+int current_device();
+int device_cus(int dev);
+// Resident blocks per CU of `kernel` (a __global__ function's address) with
+// `threads` threads and `lds_bytes` of dynamic LDS, on device `dev`.
+int cached_blocks_per_cu(int dev, const void* kernel, int threads, int lds_bytes);
+
+// moe_permute_fwd's argument checks and launches, with a caller-chosen
+// histogram workspace of at least moe_permute_workspace_bytes(T * k,
+// num_buckets) bytes (permute.hip).
+int permute_fwd_run(const void* hidden, int64_t T, int64_t H, const int64_t* ids, int64_t k, int64_t divisor,
+                    int64_t num_buckets, void* permuted, int32_t* perm, int32_t* pos_of_slot, int32_t* counts,
+                    int32_t* offsets, void* workspace, size_t workspace_bytes, void* stream);
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

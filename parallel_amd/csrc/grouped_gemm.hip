@@ -181,9 +181,12 @@ __device__ int2 kg_cost_split(const int32_t* offs, int G, int rows, int per_grou
 }
 
 // Tile configurations: BK-deep k-tiles staged through a STAGES-deep LDS ring.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
+// PIPE selects the software-pipelined k-loop of the one-wave-per-SIMD
+// layouts (each wave reads the next 16-deep half step's fragments while its
+// MFMAs run; one barrier per k-step, between the halves).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int PIPE_ = 0>
 struct TileCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_, PIPE = PIPE_;
   static constexpr int kThreads = 64 * WM * WN;
 };
 // Expert GEMMs and weight gradients: 160 KiB ring, 8 waves.
@@ -194,6 +197,15 @@ using BigTile = TileCfg<256, 256, 32, 2, 4, 5>;
 using TallTile = TileCfg<384, 128, 32, 4, 2, 5>;
 // Router GEMMs (N = E = 128): 80 KiB ring, 4 waves (two workgroups per CU).
 using SmallTile = TileCfg<128, 128, 32, 2, 2, 5>;
+// Expert GEMMs, one wave per SIMD: 128x128 wave tiles (16 accumulator
+// sub-tiles, 256 fp32 registers per lane), so a k-step reads 64 KiB of
+// fragments from LDS per CU instead of the 96 KiB of 128x64 wave tiles; with
+// the 32 KiB of DMA writes that is 96 of the 128 bytes per clock the LDS
+// serves at the MFMA peak, where eight 128x64 waves would need all 128.
+using BigTile4 = TileCfg<256, 256, 32, 2, 2, 5, 1>;
+// The same loop on eight 128x64 waves (two per SIMD).
+using BigTileP = TileCfg<256, 256, 32, 2, 4, 5, 1>;
+using TallTileP = TileCfg<384, 128, 32, 4, 2, 5, 1>;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
@@ -305,9 +317,10 @@ __device__ __forceinline__ constexpr int stg_swizzle(int r) { return (((r >> 1) 
 // Store instructions per wave per epilogue (all issued unconditionally).
 template <int EPI, int WTM, int SM, int SN>
 constexpr int epilogue_stores() {
+  // bf16 outputs are staged one 32-row x 64-column pass at a time
   return EPI == EPI_F32            ? SM * SN * 4
-         : EPI == EPI_SWIGLU_FWD  ? (WTM / 16) * 3
-                                  : WTM / 8;  // EPI_BF16; EPI_WGRAD (its fp32 variant issues more)
+         : EPI == EPI_SWIGLU_FWD  ? (WTM / 16) * 3 * (SN / 2)
+                                  : (WTM / 8) * (SN / 2);  // EPI_BF16; EPI_WGRAD (its fp32 variant issues more)
 }
 
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
@@ -331,17 +344,30 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // stage read three steps earlier, which every wave had left by the last
   // barrier.  Shallower rings synchronise every step with the DMA
   // STAGES - 1 steps ahead.
-  constexpr bool PAIR = STAGES == 5;
-  constexpr int LEAD = PAIR ? STAGES - 2 : STAGES - 1;
-  constexpr int WAIT = PAIR ? LPW : (STAGES - 2) * LPW;        // DMA younger than the k-tiles waited for
-  constexpr int RELAX = PAIR ? 2 : STAGES - 1;                 // waits that an epilogue's stores precede
+  //
+  // The pipelined loop (CFG::PIPE) keeps the 5-deep ring with the DMA 3
+  // k-steps ahead but synchronises once per k-step, in its middle: iteration
+  // c reads the second half step of k-tile c, multiplies the first, waits for
+  // k-tile c + 1 and synchronises, reads the first half step of c + 1 and
+  // multiplies the second half of c.  Half of the DMA of k-tile c + 3 is
+  // fired among each half's MFMAs.  Its stage last held k-tile c - 2, whose
+  // fragments every wave had consumed (waited for) before the barrier in the
+  // middle of iteration c - 1, and both halves of iteration c come after that
+  // barrier.  The DMA younger than the k-tile waited for is k-tile c + 2 and
+  // the first half of c + 3.
+  constexpr bool PIPE = CFG::PIPE != 0;
+  constexpr bool PAIR = STAGES == 5 && !PIPE;
+  constexpr int LEAD = (PAIR || PIPE) ? STAGES - 2 : STAGES - 1;
+  constexpr int WAIT = PIPE ? LPW + LPW / 2 : PAIR ? LPW : (STAGES - 2) * LPW;  // DMA younger than the k-tile waited for
+  constexpr int RELAX = (PAIR || PIPE) ? 2 : STAGES - 1;                       // waits that an epilogue's stores precede
   constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
-  constexpr int SLOT = 32 * WTN * 2;                           // staging bytes per wave (one 32-row pass)
+  constexpr int SLOT = 32 * 64 * 2;  // staging bytes per wave (one 32-row x 64-column pass)
   static_assert(BK == 32 || BK == 64, "swizzles and DMA mapping cover 32- and 64-deep k-tiles");
   constexpr int RB = BK * 2;      // bytes per K-contiguous row of a k-tile
   constexpr int CPR = BK / 8;     // 16-byte chunks per K-contiguous row
   constexpr int RPI = 64 / CPR;   // K-contiguous rows per DMA instruction
-  static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
+  static_assert(WTM % 32 == 0 && (WTN == 64 || WTN == 128), "wave tiles are whole 32x32 sub-tiles, 64 or 128 columns wide");
+  static_assert(!PIPE || (STAGES == 5 && LPW % 2 == 0 && BK == 32), "the pipelined loop's stage and DMA schedule");
   static_assert(NI_A % NWAVES == 0 && NI_B % NWAVES == 0, "DMA instructions of each operand split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
   static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
@@ -560,14 +586,15 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         } else {
           int wrow;
           if constexpr (EPI == EPI_SWIGLU_FWD) {
-            // Tile row r -> (wave column, sub-tile, half): the first SN/2
-            // sub-tiles of each wave column are gate rows, the rest the
-            // matching up rows.
+            // Tile row r -> (wave column, 64-column group, half): each
+            // 64-column group of a wave tile holds 32 gate rows, then the
+            // 32 matching up rows, so that one 64-column epilogue pass sees
+            // both halves of its act columns.
             const int wcol = r / WTN;
             const int within = r % WTN;
-            const int sn = within / 32;
-            const int half = sn / (SN / 2);
-            const int act_col = (dt.n0 / 2) + wcol * (WTN / 2) + (sn % (SN / 2)) * 32 + (within % 32);
+            const int group = within / 64;
+            const int half = (within % 64) / 32;
+            const int act_col = (dt.n0 / 2) + wcol * (WTN / 2) + group * 32 + (within % 32);
             ok = act_col < p.swiglu_I;
             wrow = half * p.swiglu_I + act_col;
           } else {
@@ -758,6 +785,16 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const __amdgpu_buffer_rsrc_t rsC2 = make_rsrc(p.C2, p.c2_bytes);  // SwiGLU pre-activation (0 bytes if absent)
 
   auto epilogue = [&](const Tile& t) __attribute__((always_inline)) {
+    if constexpr (PIPE && NWAVES == 4) {
+      // The 256 accumulator registers of a 128x128 wave tile live in AGPRs.
+      // Without this fence the compiler copies every accumulator to a VGPR
+      // right after its last MFMA, in the k-loop, for the conditional
+      // epilogue, which doubles their footprint and spills the k-loop.
+#pragma unroll
+      for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) asm volatile("" : "+a"(acc[i][j]));
+    }
     const int wcol0 = t.n0 + wn * WTN;
     const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
     // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
@@ -802,8 +839,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     const int stg_lane = l32 * 128 + ((khalf ^ ((l32 >> 4) & 1)) << 3);
     const int stg_swz = stg_swizzle(l32);
     const int rr8 = lane >> 3, c8 = lane & 7;  // row-read lane mapping: row 8n + rr8, chunk c8
+    // One pass per 32 rows (row sub-tile i) and 64 columns (column group h:
+    // sub-tiles 2h and 2h + 1).
 #pragma unroll
-    for (int i = 0; i < SM; ++i) {
+    for (int ih = 0; ih < SM * (SN / 2); ++ih) {
+      const int i = ih / (SN / 2), h = ih % (SN / 2);
+      const int pcol0 = wcol0 + 64 * h;     // first output column of this pass
       const int prow0 = t.m0 + sub_row(i);  // first output row of this pass
       // Output offsets of this pass's row reads and, when accumulating, the
       // existing gradient, loaded before the staging so that their latency
@@ -812,7 +853,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
       uint4 in0[4];
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const int row = prow0 + 8 * n + rr8, col = wcol0 + c8 * 8;
+        const int row = prow0 + 8 * n + rr8, col = pcol0 + c8 * 8;
         const bool ok = row < row_limit && col < p.N;
         out_off[n] = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldc) + static_cast<uint32_t>(col)) * 2u
                         : kOOB;
@@ -821,13 +862,14 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         }
       }
 #pragma unroll
-      for (int j = 0; j < SN; ++j)
+      for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          const int j = 2 * h + jj;
           uint2 v;
           v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
           v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          *reinterpret_cast<uint2*>(slot + stg_lane + (((j * 4 + q) ^ stg_swz) << 4)) = v;
+          *reinterpret_cast<uint2*>(slot + stg_lane + (((jj * 4 + q) ^ stg_swz) << 4)) = v;
         }
       if constexpr (EPI == EPI_SWIGLU_FWD) {
         // Slot columns 0-31 are gate, 32-63 the matching up columns.  A lane
@@ -835,7 +877,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         // with the reference's bf16 roundings (bf16 GEMM output, silu output,
         // product); gate | up go to the saved pre-activation.
         const int rr = lane >> 2, c4 = lane & 3;
-        const int act_col = (t.n0 / 2) + wn * (WTN / 2) + c4 * 8;
+        const int act_col = (t.n0 / 2) + wn * (WTN / 2) + 32 * h + c4 * 8;
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
           const int r = 16 * n + rr;
@@ -941,7 +983,101 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   for (int s = 0; s < LEAD; ++s) dma_issue(s);
   int cstage = 0, dstage = LEAD;
   int parity = 0;  // k-step count of the stream, mod 2
-  if (any) {
+  if constexpr (PIPE) {
+    // One wave per SIMD: the matrix pipe is fed only while this wave issues
+    // MFMAs, so the fragments of the next half step are read into the other
+    // register set while the current half step's MFMAs run, and the block
+    // barrier sits where the wave has just issued a run of MFMAs.
+    constexpr int HALF = LPW / 2;  // DMA instructions fired among one half step's MFMAs
+    bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
+    auto read_half = [&](bf16x8_t (&fa)[SM], bf16x8_t (&fb)[SN], const char* stage, int ks)
+                         __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < SM; ++i) {
+        if constexpr (A_KC) {
+          fa[i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * WM * 32 * RB);
+        } else {
+          const char* q = stage + a_mc[i] + 16 * ks * BM * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(q + 4 * BM * 2));
+          fa[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SN; ++j) {
+        if constexpr (B_KC) {
+          fb[j] = *reinterpret_cast<const bf16x8_t*>(stage + b_kc[ks] + j * 32 * RB);
+        } else {
+          const char* q = stage + b_mc[j] + 16 * ks * BN * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)q);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(q + 4 * BN * 2));
+          fb[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+    };
+    // One half step's MFMAs over the first `na` row sub-tiles, with DMA slots
+    // slot0 .. slot0 + HALF - 1 fired between the row groups.
+    auto mfma_half = [&](const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN], int na, int slot0)
+                         __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < SM; ++i) {
+        if (i < na) {
+#pragma unroll
+          for (int j = 0; j < SN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < HALF; ++s2) {
+          if ((s2 * SM) / HALF == i) {
+            __builtin_amdgcn_sched_barrier(0);
+            dma_fire(slot0 + s2);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    };
+    if (any) {
+      // k-tile 0 landed (all but k-tiles 1 and 2 of this wave's DMA), then everyone's.
+      wait_vmcnt<2 * LPW>();
+      barrier();
+      read_half(fa0, fb0, ring, 0);
+      for (;;) {
+        const char* cur = ring + cstage * STAGE_BYTES;
+        const int nstage = cstage + 1 == STAGES ? 0 : cstage + 1;
+        read_half(fa1, fb1, cur, 1);
+        dma_prepare(dstage);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(fa0, fb0, n_act, 0);
+        // k-tile c + 1 landed: this wave's DMA (all but the WAIT younger
+        // instructions, plus the last epilogue's stores while they drain),
+        // then every wave's, via the barrier.
+        const bool drain = relax > 0;
+        if (relax > 0) --relax;
+        if (drain) {
+          wait_vmcnt<WAIT + NST>();
+        } else {
+          wait_vmcnt<WAIT>();
+        }
+        barrier();
+        read_half(fa0, fb0, ring + nstage * STAGE_BYTES, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(fa1, fb1, n_act, HALF);
+        dma_advance();
+        dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
+        cstage = nstage;
+        if (++ck == ct.nk) {
+          // Stage the tile through the ring stage of its last k-tile: after
+          // this barrier every wave has consumed its fragments, and the DMA
+          // reaches that stage only two barriers later.
+          slot = ring + (cstage == 0 ? STAGES - 1 : cstage - 1) * STAGE_BYTES + wave * SLOT;
+          barrier();
+          epilogue(ct);
+          relax = RELAX;
+          if (!compute_seek(cj + 1)) break;
+        }
+      }
+    }
+  } else if (any) {
     for (;;) {
       // k-tiles of this step (and, pairwise, the next) landed: this wave's
       // DMA (all but the WAIT younger instructions, plus the last epilogue's
@@ -1003,19 +1139,6 @@ int set_bytes(GemmParams& p, int64_t a_bytes, int64_t b_bytes, int64_t c_bytes, 
   return MOE_OK;
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 template <int MODE, bool B_KCONTIG, int EPI, class CFG>
 int launch(GemmParams& p, hipStream_t stream, const char* name) {
   if (p.k_splits < 1) {
@@ -1043,15 +1166,10 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
   p.total_tiles = static_cast<int>(tiles);
   // Persistent grid: as many blocks as fit at once (capped by the tile
   // count), a multiple of the XCD count.
-  static int occ = 0;
-  if (!occ) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>,
-                                                     CFG::kThreads, 0) != hipSuccess || n <= 0)
-      n = 1;
-    occ = n;
-  }
-  const int64_t resident = static_cast<int64_t>(device_cus()) * occ / kNumXcd * kNumXcd;
+  const int dev = current_device();
+  const int occ = cached_blocks_per_cu(dev, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE, B_KCONTIG, EPI, CFG>),
+                                       CFG::kThreads, 0);
+  const int64_t resident = static_cast<int64_t>(device_cus(dev)) * occ / kNumXcd * kNumXcd;
   const int grid = static_cast<int>(std::max<int64_t>(kNumXcd, std::min<int64_t>(round_up(static_cast<int>(tiles),
                                                                                           kNumXcd),
                                                                                  resident)));
@@ -1069,6 +1187,7 @@ template <bool B_KCONTIG, int EPI>
 int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   const int out_cols = (EPI == EPI_SWIGLU_FWD) ? 2 * p.swiglu_I : p.N;
   if (out_cols <= 1024) return launch<MODE_MG, B_KCONTIG, EPI, TallTile>(p, stream, name);
+  if constexpr (B_KCONTIG) return launch<MODE_MG, B_KCONTIG, EPI, BigTileP>(p, stream, name);
   return launch<MODE_MG, B_KCONTIG, EPI, BigTile>(p, stream, name);
 }
 
@@ -1162,11 +1281,15 @@ int router_dgrad(const bf16_t* dl, const bf16_t* wr, bf16_t* dx, int T, int H, i
 // half holds d_act (the bf16 input-gradient GEMM output) on entry; on exit
 // d_pre = (d_gate | d_up) with the reference's bf16 roundings:
 //   d_up = d * silu(gate),  d_silu = d * up,  d_gate = d_silu * s (1 + gate (1 - s)).
-// One lane per 8 columns (16-byte loads and stores).
+// One lane per 8 columns (16-byte loads and stores).  Only the rows of the
+// groups, [0, offs[G-1]), are touched (read on the device, no host sync): the
+// sentinel tail past them holds no pre-activations and stays as it is.
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(bf16_t* __restrict__ d_pre, const bf16_t* __restrict__ pre,
-                                                         unsigned rows, unsigned I) {
+                                                         const int32_t* __restrict__ offs, int G, unsigned rows,
+                                                         unsigned I) {
   const unsigned cpr = I / 8;  // 8-column chunks per half row
-  const unsigned total = rows * cpr;
+  const unsigned valid = offs ? static_cast<unsigned>(min(max(offs[G - 1], 0), static_cast<int>(rows))) : rows;
+  const unsigned total = valid * cpr;
   for (unsigned c = blockIdx.x * blockDim.x + threadIdx.x; c < total; c += gridDim.x * blockDim.x) {
     const unsigned r = c / cpr, k = (c - r * cpr) * 8;
     bf16_t* dr = d_pre + static_cast<size_t>(r) * 2 * I;
@@ -1317,7 +1440,8 @@ extern "C" int moe_grouped_gemm_dgrad_swiglu_bwd(const void* dy, const void* w_d
   const int64_t chunks = M * I / 8;
   const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 4096));
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(grid), dim3(256), 0, st, static_cast<bf16_t*>(d_pre),
-                     static_cast<const bf16_t*>(pre), static_cast<unsigned>(M), static_cast<unsigned>(I));
+                     static_cast<const bf16_t*>(pre), offs, static_cast<int>(G), static_cast<unsigned>(M),
+                     static_cast<unsigned>(I));
   return launch_status("moe_grouped_gemm_dgrad_swiglu_bwd (swiglu)");
 }
 

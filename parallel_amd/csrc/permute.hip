@@ -28,9 +28,14 @@ constexpr int kPermThreads = 256;  // 4 waves
 constexpr int kPerThread = kChunk / kPermThreads;
 constexpr int kMaxBuckets = 1024;  // real buckets; +1 for the sentinel bucket
 
+// Bucket = floor(id / divisor) (divisor >= 1), as the reference's owner rule
+// (torch.div rounding_mode="floor"); a negative id is below bucket 0 and goes
+// to the sentinel bucket with the ids past the last bucket.  (C++ division
+// truncates toward zero and would put -1 in bucket 0 for divisor > 1.)
 __device__ __forceinline__ int bucket_of(int64_t id, int64_t divisor, int nb) {
-  int64_t b = id / divisor;
-  return (b < 0 || b >= nb) ? nb : static_cast<int>(b);
+  if (id < 0) return nb;
+  const int64_t b = id / divisor;
+  return b >= nb ? nb : static_cast<int>(b);
 }
 
 __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(const int64_t* __restrict__ ids, int S,
@@ -199,8 +204,10 @@ __global__ void dispatch_meta_kernel(const int64_t* __restrict__ ids, const floa
   for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < S; pos += gridDim.x * blockDim.x) {
     int s = perm[pos];
     if (local_ids) {
-      int64_t id = ids[s];
-      local_ids[pos] = id - (id / divisor) * divisor;
+      // id - floor(id / divisor) * divisor (the reference's send_experts), in [0, divisor)
+      const int64_t id = ids[s];
+      const int64_t r = id % divisor;
+      local_ids[pos] = r < 0 ? r + divisor : r;
     }
     if (routed_scores) routed_scores[pos] = scores[s];
   }
@@ -279,6 +286,16 @@ extern "C" int moe_permute_fwd(const void* hidden, int64_t T, int64_t H, const i
                                int64_t divisor, int64_t num_buckets, void* permuted, int32_t* perm,
                                int32_t* pos_of_slot, int32_t* counts, int32_t* offsets, void* workspace,
                                size_t workspace_bytes, void* stream) {
+  return moe::permute_fwd_run(hidden, T, H, ids, k, divisor, num_buckets, permuted, perm, pos_of_slot, counts,
+                              offsets, workspace, workspace_bytes, stream);
+}
+
+namespace moe {
+// Validates and launches moe_permute_fwd's kernels with the given histogram
+// workspace (moe_permute_workspace_bytes(T * k, num_buckets) bytes at least).
+int permute_fwd_run(const void* hidden, int64_t T, int64_t H, const int64_t* ids, int64_t k, int64_t divisor,
+                    int64_t num_buckets, void* permuted, int32_t* perm, int32_t* pos_of_slot, int32_t* counts,
+                    int32_t* offsets, void* workspace, size_t workspace_bytes, void* stream) {
   MOE_REQUIRE(T >= 0 && k >= 1 && k <= 16 && T * k < (1ll << 31), MOE_ERR_INVALID,
               "permute: bad T=%lld k=%lld", (long long)T, (long long)k);
   MOE_REQUIRE(divisor >= 1, MOE_ERR_INVALID, "permute: divisor must be >= 1");
@@ -316,6 +333,7 @@ extern "C" int moe_permute_fwd(const void* hidden, int64_t T, int64_t H, const i
   }
   return rc;
 }
+}  // namespace moe
 
 extern "C" int moe_dispatch_meta(const int64_t* ids, const float* scores, const int32_t* perm, int64_t S,
                                  int64_t divisor, int64_t* local_ids, float* routed_scores, void* stream) {

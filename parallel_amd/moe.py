@@ -76,12 +76,19 @@ def mi355x_experts_forward(self, hidden_states: Tensor, top_k_index: Tensor, top
     _check_gated_silu(self)
     if self.gate_up_proj.shape[0] != self.num_experts:
         raise ValueError(f"gate_up_proj holds {self.gate_up_proj.shape[0]} experts, module says {self.num_experts}")
-    out = ops.experts(hidden_states, top_k_index, top_k_weights, self.gate_up_proj, self.down_proj)
+    out = ops.experts(hidden_states, top_k_index, top_k_weights, self.gate_up_proj, self.down_proj,
+                      accumulate_grad=bool(getattr(self, "fuse_grad_accumulation", False)))
     return out.to(hidden_states.dtype)
 
 
 class Experts(nn.Module):
-    """Qwen3MoeExperts parameters, forward on the gfx950 grouped-GEMM path."""
+    """Qwen3MoeExperts parameters, forward on the gfx950 grouped-GEMM path.
+
+    ``fuse_grad_accumulation`` (off by default) adds each backward's weight
+    gradients into existing ``.grad`` tensors inside the weight-gradient GEMM
+    (see ``ops.experts``); it skips the parameters' post-accumulate-grad hooks."""
+
+    fuse_grad_accumulation = False
 
     def __init__(self, config):
         super().__init__()

@@ -415,11 +415,13 @@ def _check_experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, g
 
 @torch.library.custom_op(f"{LIB}::experts_fwd", mutates_args=())
 def experts_fwd(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
-                down_proj: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+                down_proj: Tensor, accumulate_grad: bool = False
+                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """grouped_mm_experts_forward (TF integrations/moe.py:377-478) on gfx950.
 
     Returns (out [T,H], and for the backward: xp [S,H], pre [S,2I], act [S,I],
-    y [S,H], pos_of_slot [S] int32, offsets [E] int32).
+    y [S,H], pos_of_slot [S] int32, offsets [E] int32).  ``accumulate_grad``
+    only changes the backward (see ``experts``).
     """
     T, H, k, E, I = _check_experts(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
     S = T * k
@@ -450,7 +452,7 @@ def experts_fwd(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate
 
 
 @experts_fwd.register_fake
-def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj):
+def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_grad=False):
     T, H = hidden.shape
     S = T * top_k_index.shape[1]
     E, I2, _ = gate_up_proj.shape
@@ -524,29 +526,82 @@ def _(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slo
 
 def _experts_setup(ctx, inputs, output):
     ctx.set_materialize_grads(False)
-    hidden, top_k_index, top_k_weights, gate_up_proj, down_proj = inputs
+    hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_grad = inputs
     _, xp, pre, act, y, pos, offsets = output
     ctx.save_for_backward(top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos, offsets)
     ctx.weights_dtype = top_k_weights.dtype
     ctx.hidden_dtype = hidden.dtype
+    # The parameters themselves (not their saved aliases): their .grad is read at backward time.
+    ctx.params = (gate_up_proj, down_proj) if accumulate_grad else None
     ctx.mark_non_differentiable(xp, pre, act, y, pos, offsets)
+
+
+def _grad_target(param: Tensor) -> Tensor | None:
+    """param.grad when the weight-gradient kernel can add into it in place."""
+    g = param.grad if param.is_leaf else None
+    if g is None or g.shape != param.shape or not g.is_contiguous() or g.device != param.device:
+        return None
+    return g if g.dtype in (BF16, torch.float32) else None
 
 
 def _experts_backward(ctx, d_out, *_unused):
     w, gu, dn, xp, pre, act, y, pos, offsets = ctx.saved_tensors
     if d_out is None:
-        return None, None, None, None, None
-    d_hidden, d_w, d_gu, d_dn = experts_bwd(d_out, w, gu, dn, xp, pre, act, y, pos, offsets)
-    return d_hidden.to(ctx.hidden_dtype), None, d_w.to(ctx.weights_dtype), d_gu, d_dn
+        return None, None, None, None, None, None
+    targets = [_grad_target(p) for p in ctx.params] if ctx.params is not None else [None, None]
+    if targets[0] is None and targets[1] is None:
+        d_hidden, d_w, d_gu, d_dn = experts_bwd(d_out, w, gu, dn, xp, pre, act, y, pos, offsets)
+    else:
+        d_hidden, d_w, d_gu, d_dn = experts_bwd_accumulate(d_out, w, gu, dn, xp, pre, act, y, pos, offsets,
+                                                           targets[0], targets[1])
+    return d_hidden.to(ctx.hidden_dtype), None, d_w.to(ctx.weights_dtype), d_gu, d_dn, None
 
 
 experts_fwd.register_autograd(_experts_backward, setup_context=_experts_setup)
 
 
+def experts_bwd_accumulate(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets,
+                           gu_grad: Tensor | None, dn_grad: Tensor | None):
+    """experts_bwd with the weight gradients added into existing gradient
+    tensors by the weight-gradient kernel's accumulate epilogue (bf16: the
+    fp32 sum rounded to bf16 plus the existing value, rounded again, as
+    torch's bf16 add; fp32 targets add the fp32 sum).  A projection whose
+    target is None gets a fresh gradient, returned as usual; the returned
+    gradient of an accumulated projection is None."""
+    E = gate_up_proj.shape[0]
+    S = xp.shape[0]
+    s = _stream(d_out)
+    params = {"gate_up_proj": (gate_up_proj, gu_grad), "down_proj": (down_proj, dn_grad)}
+
+    def wgrad(name, dc, a, n, k):
+        param, target = params[name]
+        tag = "up_wgrad" if name == "gate_up_proj" else "down_wgrad"
+        if target is None:
+            dw = torch.empty_like(param)
+            call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s, tag=tag)
+            return dw
+        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(target),
+             int(target.dtype == torch.float32), 1, s, tag=tag)
+        return None
+
+    return experts_bwd_kernels(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets,
+                               wgrad)
+
+
 def experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
-            down_proj: Tensor) -> Tensor:
-    """Differentiable expert layer output [T,H] (TF integrations/moe.py:377-478 contract)."""
-    return experts_fwd(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)[0]
+            down_proj: Tensor, accumulate_grad: bool = False) -> Tensor:
+    """Differentiable expert layer output [T,H] (TF integrations/moe.py:377-478 contract).
+
+    With ``accumulate_grad`` a weight that is a leaf and already holds a
+    ``.grad`` (bf16 or fp32, its shape, contiguous) gets this backward's
+    weight gradient added into that tensor by the weight-gradient GEMM itself,
+    instead of a separate dense gradient that autograd then adds (the
+    reference's accumulation, parallel/parallel/engine/engine.py:165-178);
+    the result is the same bits.  Autograd sees no gradient for such a weight,
+    so its post-accumulate-grad hooks do not run: leave it off where an FSDP
+    unit waits for those hooks (parallel/parallel/engine/_dp_param_unit.py:669-690).
+    A weight without a ``.grad`` gets a fresh gradient as usual."""
+    return experts_fwd(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_grad)[0]
 
 
 # ------------------------------------------------------- token dispatch ops

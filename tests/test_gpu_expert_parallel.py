@@ -1,0 +1,134 @@
+"""Expert parallelism on the GPU: both hook runtimes installed on a model of
+SparseMoeBlock layers, one rank's share at a time, on the kernels; the
+dispatcher's owner-major send buffer against the oracle's restatement of
+TokenDispatcher.dispatch (token_dispatch.py:101-125), bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from conftest import GOLDEN, close_bf16
+from oracle import moe_oracle as O
+from parallel_amd import (
+    ExpertPartition,
+    Experts,
+    ReplicatedTokenExpertParallel,
+    SequenceParallelExpertParallel,
+    SparseMoeBlock,
+    ops,
+    verify_expert_modules,
+)
+from parallel_amd.workloads import WORKLOADS, make_block_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+class _Layer(nn.Module):
+    def __init__(self, block):
+        super().__init__()
+        self.mlp = block
+
+
+def ep_model(w, inp, ep, rank, layers=2):
+    """A model whose decoder layers hold SparseMoeBlocks with the full router
+    and rank ``rank``'s slice of the experts (dim-0 EXPERT placement,
+    parallel/parallel/engine/model_parallel/models/qwen3_moe.py:64-65,81-84)."""
+    part = ExpertPartition(w.experts, ep, rank)
+    cfg = w.config()
+    local_cfg = w.config()
+    local_cfg.num_experts = part.local_count
+    model = nn.Module()
+    model.layers = nn.ModuleList()
+    for _ in range(layers):
+        block = SparseMoeBlock(cfg)
+        block.experts = Experts(local_cfg)
+        with torch.no_grad():
+            block.gate.weight.copy_(inp["router_weight"])
+            block.experts.gate_up_proj.copy_(inp["gate_up_proj"][part.start:part.stop])
+            block.experts.down_proj.copy_(inp["down_proj"][part.start:part.stop])
+        model.layers.append(_Layer(block))
+    return model.to(DEV, BF), part
+
+
+def run_share(runtime_cls, w, inp, ep, rank):
+    """Forward + backward of <block(x), d_out> through the first layer of the
+    model with ``runtime_cls`` installed for (ep, rank)."""
+    model, part = ep_model(w, inp, ep, rank)
+    verify_expert_modules(model, part)
+    rt = runtime_cls(part, None)
+    rt.apply(model)
+    x = inp["x"].to(DEV).view(1, w.tokens, w.hidden).requires_grad_()
+    block = model.layers[0].mlp
+    out = block(x)
+    out.backward(inp["d_out"].to(DEV).view_as(out))
+    torch.cuda.synchronize()
+    rt.close()
+    return out.detach().view(w.tokens, w.hidden), x.grad.view(w.tokens, w.hidden), block.gate.weight.grad
+
+
+@pytest.mark.parametrize("runtime_cls", [ReplicatedTokenExpertParallel, SequenceParallelExpertParallel])
+def test_ep2_shares_against_golden_and_oracle(runtime_cls):
+    """C1 block at ep = 2: rank 0's share equals transformers' experts on the
+    localized routes (golden sentinel_out); each rank's share equals the
+    oracle's experts on that rank's localized routes; the shares' outputs,
+    input gradients and router gradients sum to the unsharded block's."""
+    w = WORKLOADS["c1"]
+    inp = make_block_inputs(w, seed=1234, dtype=BF)
+    ref = O.block_forward_backward(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"],
+                                   inp["d_out"], top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=0.0)
+    g = np.load(GOLDEN / "c1_qwen3_moe_block.npz")
+    ep = 2
+    outs, dxs, drs = [], [], []
+    for rank in range(ep):
+        out, dx, dr = run_share(runtime_cls, w, inp, ep, rank)
+        part = ExpertPartition(w.experts, ep, rank)
+        li, ls, _ = part.localize_routes(ref["indices"], ref["scores"])
+        want = O.experts_grouped(inp["x"].float(), li, ls, inp["gate_up_proj"][part.start:part.stop].float(),
+                                 inp["down_proj"][part.start:part.stop].float())
+        close_bf16(out, want, f"rank {rank} share")
+        if rank == 0:
+            close_bf16(out, torch.from_numpy(g["sentinel_out"]), "rank 0 share vs transformers")
+        outs.append(out.float().cpu())
+        dxs.append(dx.float().cpu())
+        drs.append(dr.float().cpu())
+    close_bf16(sum(outs), ref["out"], "sum of shares")
+    close_bf16(sum(dxs), ref["dx"], "sum of input gradients")
+    close_bf16(sum(drs), ref["d_router"], "sum of router gradients")
+
+
+def test_both_runtimes_give_the_same_share():
+    """The replicated-token and the dispatch runtimes compute the same rank
+    share by different kernel sequences (sentinel slots skipped in place,
+    against owner-major dispatch and gather-form combine)."""
+    w = WORKLOADS["c1"]
+    inp = make_block_inputs(w, seed=77, dtype=BF)
+    for ep, rank in ((4, 1), (8, 7)):
+        a = run_share(ReplicatedTokenExpertParallel, w, inp, ep, rank)
+        b = run_share(SequenceParallelExpertParallel, w, inp, ep, rank)
+        for name, x, y in zip(("out", "dx", "d_router"), a, b):
+            close_bf16(x, y, f"ep {ep} rank {rank} {name}")
+
+
+@pytest.mark.parametrize("T,E,local,seed", [(512, 128, 16, 0), (1000, 64, 8, 1), (37, 16, 4, 2), (256, 8, 1, 3)])
+def test_dispatch_send_buffer_bit_exact(T, E, local, seed):
+    """ops.dispatch_fwd at ep = E / local equals TokenDispatcher.dispatch's send
+    side (the oracle's restatement) bit for bit: rows, local expert ids,
+    scores, source tokens and splits."""
+    H, k = 64, 4 if E >= 4 else E
+    g = torch.Generator().manual_seed(seed)
+    hidden = torch.randn(T, H, generator=g).to(BF)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    scores = torch.rand(T, k, generator=g)
+    ep = E // local
+    sh, se, ss, src, pos, counts = ops.dispatch_fwd(hidden.to(DEV), idx.to(DEV), scores.to(DEV), local, ep)
+    rh, re, rs, rsrc, rsplits = O.dispatch_send(hidden, idx, scores, local, ep)
+    assert torch.equal(sh.cpu(), rh)
+    assert torch.equal(se.cpu(), re)
+    assert torch.equal(ss.cpu(), rs)
+    assert torch.equal(src.cpu(), rsrc)
+    assert tuple(counts.cpu().tolist()) == rsplits
+    # pos_of_slot is the inverse of the send order
+    assert torch.equal(src.cpu()[pos.cpu().long()], torch.arange(T).repeat_interleave(k))

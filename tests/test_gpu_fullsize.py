@@ -1,0 +1,122 @@
+"""The benchmark configurations at full size on the GPU, backward included,
+through size-independent properties (the CPU oracle cannot run these sizes
+in seconds):
+
+* every expert's weight gradients and input gradients against plain fp32
+  torch.mm references of the same products, computed per expert on the GPU
+  from the kernels' own inputs (d_pre and xp, dy and act): the persistent
+  schedules' multi-round tile loops, the even m-split of large experts and
+  the cost split of the weight gradients at 128 experts, all at full size;
+* weight-gradient accumulation into existing gradients, fused in the kernel
+  against torch's separate add, bit for bit.
+"""
+
+import pytest
+import torch
+
+from conftest import close_bf16
+from parallel_amd import _lib, ops
+from parallel_amd.workloads import WORKLOADS, make_block_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _forward(w, seed):
+    inp = make_block_inputs(w, seed=seed, device=DEV, dtype=BF, weights_on_device_rng=True)
+    bias = inp.get("logit_bias")
+    logits, scores, idx = ops.router_fwd(inp["x"], inp["router_weight"], w.top_k, w.norm_topk_prob, bias)
+    saved = ops.experts_fwd(inp["x"], idx, scores, inp["gate_up_proj"], inp["down_proj"])
+    return inp, scores, idx, saved
+
+
+def _dgrad(dc, wt, offsets, G, M, N, K):
+    """moe_grouped_gemm_dgrad: da[M,K] = dc[M,N] . w[g] (w [G,N,K])."""
+    da = torch.empty(M, K, dtype=BF, device=DEV)
+    _lib.call("moe_grouped_gemm_dgrad", dc.data_ptr(), wt.data_ptr(), offsets.data_ptr(), G, M, N, K, da.data_ptr(),
+              _lib.stream_of(dc))
+    return da
+
+
+def close_on_device(actual, expected, name, max_rel=2e-2, min_cos=0.9999):
+    """close_bf16's bar (normwise max relative error, cosine) evaluated on the GPU."""
+    a = actual.float().reshape(-1)
+    b = expected.float().reshape(-1)
+    denom = float(b.abs().max())
+    rel = float((a - b).abs().max()) / max(denom, 1e-30)
+    cos = float(torch.dot(a.double(), b.double()) / (a.double().norm() * b.double().norm()).clamp_min(1e-300))
+    assert torch.isfinite(a).all(), f"{name}: non-finite values"
+    assert rel <= max_rel and (cos >= min_cos or denom == 0), f"{name}: max rel err {rel:.3e}, cosine {cos:.6f}"
+    return rel
+
+
+@pytest.mark.parametrize("name,seed", [("c2", 31), ("c4", 32), ("c5", 33)])
+def test_full_size_backward_every_expert(name, seed):
+    w = WORKLOADS[name]
+    E, H, I, S = w.experts, w.hidden, w.intermediate, w.slots
+    inp, scores, idx, saved = _forward(w, seed)
+    out, xp, pre, act, y, pos, offsets = saved
+    d_out = torch.randn(w.tokens, H, generator=torch.Generator(device=DEV).manual_seed(seed), device=DEV).to(BF)
+    captured = {}
+
+    def wgrad(proj, dc, a, n, k):
+        captured[proj] = (dc, a)
+        dw = torch.empty(E, n, k, dtype=BF, device=DEV)
+        _lib.call("moe_grouped_gemm_wgrad", dc.data_ptr(), a.data_ptr(), offsets.data_ptr(), E, S, n, k,
+                  dw.data_ptr(), 0, 0, _lib.stream_of(dc))
+        return dw
+
+    d_hidden, d_w, d_gu, d_dn = ops.experts_bwd_kernels(d_out, scores, inp["gate_up_proj"], inp["down_proj"], xp,
+                                                        pre, act, y, pos, offsets, wgrad)
+    d_pre, _ = captured["gate_up_proj"]
+    dy, _ = captured["down_proj"]
+    gu, dn = inp["gate_up_proj"], inp["down_proj"]
+    d_act = _dgrad(dy, dn, offsets, E, S, H, I)
+    d_xp = _dgrad(d_pre, gu, offsets, E, S, 2 * I, H)
+    torch.cuda.synchronize()
+    off = offsets.cpu().long().tolist()
+    assert off[-1] == S
+    counts = [off[0]] + [off[e] - off[e - 1] for e in range(1, E)]
+    assert max(counts) > 256, "some expert must span several m-tiles"
+    worst = {}
+    r0 = 0
+    for e in range(E):
+        r1 = off[e]
+        rows = slice(r0, r1)
+        if r1 == r0:
+            assert not d_gu[e].any() and not d_dn[e].any(), f"{name} expert {e}: empty expert needs zero dW"
+        else:
+            f = lambda t: t[rows].float()  # noqa: E731
+            checks = (("d_gate_up", d_gu[e], f(d_pre).t() @ f(xp)), ("d_down", d_dn[e], f(dy).t() @ f(act)),
+                      ("d_xp", d_xp[rows], f(d_pre) @ gu[e].float()), ("d_act", d_act[rows], f(dy) @ dn[e].float()))
+            for label, got, ref in checks:
+                rel = close_on_device(got, ref, f"{name} expert {e} ({r1 - r0} rows) {label}")
+                worst[label] = max(worst.get(label, 0.0), rel)
+        r0 = r1
+    print(f"{name}: worst normwise max rel err per product over {E} experts: {worst}")
+    assert torch.isfinite(d_hidden.float()).all() and torch.isfinite(d_w).all()
+
+
+def test_full_c4_gradient_accumulation_fused_equals_torch_add():
+    """C4 ("dW accumulation"): two backward steps into existing gradients.
+    The in-kernel accumulation gives the same bits as torch adding a fresh
+    dense gradient into .grad."""
+    w = WORKLOADS["c4"]
+    inp = make_block_inputs(w, seed=41, device=DEV, dtype=BF, weights_on_device_rng=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    d_outs = [torch.randn(w.tokens, w.hidden, generator=g, device=DEV).to(BF) for _ in range(2)]
+    init = [torch.randn(p.shape, generator=g, device=DEV).mul_(1e-3).to(BF)
+            for p in (inp["gate_up_proj"], inp["down_proj"])]
+    logits, scores, idx = ops.router_fwd(inp["x"], inp["router_weight"], w.top_k, True, inp["logit_bias"])
+    grads = {}
+    for fused in (False, True):
+        gu = inp["gate_up_proj"].clone().requires_grad_()
+        dn = inp["down_proj"].clone().requires_grad_()
+        gu.grad, dn.grad = init[0].clone(), init[1].clone()
+        for d_out in d_outs:
+            ops.experts(inp["x"], idx, scores, gu, dn, accumulate_grad=fused).backward(d_out)
+        torch.cuda.synchronize()
+        grads[fused] = (gu.grad, dn.grad)
+    for a, b, label in zip(grads[True], grads[False], ("d_gate_up", "d_down")):
+        assert torch.equal(a, b), f"fused {label} accumulation differs from torch's add"

@@ -6,7 +6,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from conftest import close_bf16
+from conftest import close_bf16, routing_check
 from oracle import moe_oracle as O
 from parallel_amd import _lib, ops
 
@@ -34,11 +34,8 @@ def test_router_topk_bit_exact_on_same_logits(T, E, k, norm):
     logits = torch.randn(T, E, generator=gen(T + E))
     scores, idx = ops.router_topk(logits.to(DEV), k, norm)
     ref_scores, ref_idx = O.topk_softmax(logits, k, norm)
-    ties = O.topk_ties(logits, ref_idx)
-    mismatch = (idx.cpu() != ref_idx).any(dim=1)
-    assert not (mismatch & ~ties).any(), f"{int((mismatch & ~ties).sum())} tokens routed differently"
-    ok = ~ties
-    torch.testing.assert_close(scores.cpu()[ok], ref_scores[ok], rtol=2e-6, atol=1e-7)
+    routing_check(idx, ref_idx, logits)
+    torch.testing.assert_close(scores.cpu(), ref_scores, rtol=2e-6, atol=1e-7)
 
 
 def test_router_topk_ties_go_to_lower_index():
@@ -58,8 +55,7 @@ def test_router_logits_match_fp32(T, H, E):
     ref = O.router_logits(x, w)
     torch.testing.assert_close(logits.cpu(), ref, rtol=1e-4, atol=1e-5)
     ref_s, ref_i = O.topk_softmax(logits.cpu(), min(8, E), True)
-    ties = O.topk_ties(logits.cpu(), ref_i)
-    assert not ((idx.cpu() != ref_i).any(1) & ~ties).any()
+    routing_check(idx, ref_i, logits)
 
 
 @pytest.mark.parametrize("norm,E,k", [(True, 16, 4), (False, 16, 4), (True, 200, 6), (False, 384, 1)])
@@ -102,6 +98,26 @@ def test_aux_loss_forward_backward(T, E, k, masked):
     (0.7 * ref).backward()
     torch.testing.assert_close(aux.cpu(), ref.detach(), rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(lg.grad.cpu(), lr.grad, rtol=1e-4, atol=1e-8)
+
+
+@pytest.mark.parametrize("case", ["small", "c2"])
+def test_aux_loss_masked_layers_match_transformers_golden(case):
+    """load_balancing_loss_func with an attention mask over several layers
+    (the per-layer expansion of a [batch, seq] padding mask) against the
+    golden loss and logits gradient that transformers' own function wrote."""
+    from conftest import GOLDEN
+    from parallel_amd import load_balancing_loss_func
+
+    g = np.load(GOLDEN / "aux_masked.npz")
+    layers, batch, seq, E, k, _ = g[f"{case}_meta"].tolist()
+    leaves = [torch.from_numpy(l).to(DEV).requires_grad_() for l in g[f"{case}_logits"]]
+    mask = torch.from_numpy(g[f"{case}_mask"]).to(DEV)
+    aux = load_balancing_loss_func(tuple(leaves), E, k, mask)
+    aux.backward()
+    torch.testing.assert_close(aux.cpu(), torch.tensor(float(g[f"{case}_aux"])), rtol=1e-5, atol=1e-6)
+    got = torch.stack([l.grad.cpu() for l in leaves])
+    want = torch.from_numpy(g[f"{case}_d_logits"])
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-8)
 
 
 def test_aux_loss_balanced_routing_is_top_k():
@@ -180,6 +196,28 @@ def test_permute_owner_buckets_give_send_splits():
     dest = ids.reshape(-1) // 16
     assert torch.equal(perm.cpu().long(), torch.argsort(dest, stable=True))
     assert torch.equal(counts.cpu().long(), torch.bincount(dest, minlength=8))
+
+
+@pytest.mark.parametrize("divisor,nb", [(1, 64), (16, 8), (3, 5)])
+def test_permute_out_of_range_ids_are_sentinels(divisor, nb):
+    """Negative ids and ids past the last bucket, at divisors above 1 too: the
+    bucket is floor(id / divisor), so -1 is below bucket 0 (not in it) and
+    sorts with the sentinels after every real bucket, as the oracle's
+    stable_permutation says."""
+    g = gen(divisor * 100 + nb)
+    T, k = 600, 4
+    ids = torch.randint(-3 * divisor, (nb + 2) * divisor, (T, k), generator=g)
+    assert (ids < 0).any() and (ids // divisor >= nb).any() and ((ids >= 0) & (ids < divisor)).any()
+    hidden = torch.randn(T, 32, generator=g).to(BF)
+    rows, perm, pos, counts, offsets = ops.permute_fwd(hidden.to(DEV), ids.to(DEV), divisor, nb, True)
+    r_perm, r_pos, r_counts, r_off = O.stable_permutation(ids.numpy(), divisor, nb)
+    assert np.array_equal(perm.cpu().numpy(), r_perm)
+    assert np.array_equal(pos.cpu().numpy(), r_pos)
+    assert np.array_equal(counts.cpu().numpy(), r_counts)
+    assert np.array_equal(offsets.cpu().numpy(), r_off)
+    n_valid = int(r_off[-1])
+    assert torch.equal(rows.cpu()[:n_valid], hidden[torch.from_numpy(r_perm[:n_valid]) // k])
+    assert not rows.cpu()[n_valid:].any()
 
 
 def test_permute_empty_input():
@@ -305,6 +343,33 @@ def test_swiglu_fwd_and_fused_backward(cnt, I, H):
         s0 += c
     (F.silu(g2) * u2).backward(torch.cat(d_act))
     close_bf16(d_pre, p.grad, "swiglu d_pre", max_rel=1e-2)
+
+
+def test_dgrad_swiglu_leaves_the_sentinel_tail_untouched():
+    """Rows past offs[G-1] (sentinel routes under EP) are neither read nor
+    written by the input-gradient GEMM or the SwiGLU backward: NaN poison in
+    pre and d_pre there stays bit for bit, and the valid rows equal a run over
+    the valid rows alone."""
+    cnt, I, H, tail = [40, 0, 71, 9], 64, 96, 57
+    counts, offs = _groups(cnt)
+    V = int(counts.sum())
+    M, G = V + tail, len(cnt)
+    dn = (torch.randn(G, H, I, generator=gen(40)) * 0.05).to(BF).to(DEV)
+    dy = torch.randn(M, H, generator=gen(41)).to(BF).to(DEV)
+    pre = torch.randn(M, 2 * I, generator=gen(42)).to(BF).to(DEV)
+    pre[V:] = float("nan")
+    d_pre = torch.full((M, 2 * I), float("nan"), dtype=BF, device=DEV)
+    poison = d_pre[V:].clone()
+    od = offs.to(DEV)
+    s = _lib.stream_of(pre)
+    _lib.call("moe_grouped_gemm_dgrad_swiglu_bwd", dy.data_ptr(), dn.data_ptr(), pre.data_ptr(), od.data_ptr(),
+              G, M, H, I, d_pre.data_ptr(), s)
+    valid = torch.empty(V, 2 * I, dtype=BF, device=DEV)
+    _lib.call("moe_grouped_gemm_dgrad_swiglu_bwd", dy.data_ptr(), dn.data_ptr(), pre.data_ptr(), od.data_ptr(),
+              G, V, H, I, valid.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert torch.equal(d_pre[V:].view(torch.int16), poison.view(torch.int16)), "sentinel rows were written"
+    assert torch.equal(d_pre[:V], valid) and torch.isfinite(valid.float()).all()
 
 
 # ------------------------------------------------------------------- combine

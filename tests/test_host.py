@@ -93,11 +93,12 @@ def test_expert_partition_contract():
 
 
 def test_token_dispatcher_contract():
-    with pytest.raises(ValueError, match="ep_size"):
-        TokenDispatcher(ExpertPartition(8, 2, 0), None)
     d = TokenDispatcher(ExpertPartition(8, 1, 0), None)
     with pytest.raises(ValueError, match="same shape"):
         d.dispatch(torch.zeros(2, 8), torch.zeros(2, 2, dtype=torch.long), torch.zeros(2, 3))
+    share = TokenDispatcher(ExpertPartition(8, 4, 2), None)
+    assert (share.world_size, share.rank) == (4, 2)
+    assert share._exchange_splits(torch.tensor([3, 0, 5, 1])) == ((3, 0, 5, 1), (0, 0, 5, 0))
 
 
 def test_aux_loss_api_edges():

@@ -159,3 +159,103 @@ def test_aux_loss_mask_of_ones_equals_unmasked():
     a = O.load_balancing_loss((logits,), 5, 2)
     b = O.load_balancing_loss((logits,), 5, 2, attention_mask=mask)
     torch.testing.assert_close(a, b)
+
+
+# ------------------------------------------------------------- tie detection
+
+
+def _ties_brute_force(probs: torch.Tensor, k: int) -> list[bool]:
+    """A token's top-k depends on how exact ties are broken iff some value is
+    held by two or more experts and fewer than k experts are strictly larger
+    (then at least one holder is selected and another holder's place is
+    ambiguous).  Counted pairwise, without sorting."""
+    out = []
+    for row in probs.tolist():
+        tied = False
+        for v in row:
+            larger = sum(1 for u in row if u > v)
+            equal = sum(1 for u in row if u == v)
+            tied |= equal >= 2 and larger < k
+        out.append(tied)
+    return out
+
+
+def test_topk_ties_constructed_cases():
+    E = 8
+    rows = {
+        "none": [3.0, 2.5, 2.0, 1.5, 1.0, 0.5, 0.0, -0.5],
+        "boundary": [3.0, 2.5, 2.0, 2.0, 1.0, 0.5, 0.0, -0.5],  # 3rd == 4th with k = 3
+        "inside": [3.0, 3.0, 2.0, 1.5, 1.0, 0.5, 0.0, -0.5],  # 1st == 2nd
+        "below": [3.0, 2.5, 2.0, 1.0, 1.0, 0.5, 0.0, -0.5],  # 4th == 5th: outside the top 3 and its boundary
+        "last_pair": [3.0, 2.5, 2.0, 1.5, 1.0, 0.5, -1.0, -1.0],
+        "all_equal": [0.0] * E,
+    }
+    logits = torch.tensor(list(rows.values()))
+    for k, expect in ((3, [False, True, True, False, False, True]), (8, [False, True, True, True, True, True]),
+                      (7, [False, True, True, True, True, True]), (1, [False, False, True, False, False, True])):
+        idx = torch.zeros(len(rows), k, dtype=torch.long)
+        got = O.topk_ties(logits, idx).tolist()
+        assert got == expect, f"k={k}: {dict(zip(rows, got))}"
+        assert got == _ties_brute_force(torch.softmax(logits, -1), k), f"k={k}: brute force disagrees"
+
+
+def test_topk_ties_matches_brute_force_on_random_and_planted_ties():
+    g = torch.Generator().manual_seed(11)
+    T, E = 400, 12
+    logits = torch.randn(T, E, generator=g)
+    # plant exact ties at random sorted positions in a third of the tokens
+    for t in range(0, T, 3):
+        order = torch.argsort(logits[t], descending=True)
+        a = int(torch.randint(0, E - 1, (1,), generator=g))
+        logits[t, order[a + 1]] = logits[t, order[a]]
+    probs = torch.softmax(logits, -1)
+    for k in (1, 2, 4, 8, 11, 12):
+        got = O.topk_ties(logits, torch.zeros(T, k, dtype=torch.long))
+        assert got.tolist() == _ties_brute_force(probs, k), f"k={k}"
+        assert 0 < int(got.sum()) <= len(range(0, T, 3)), "only planted ties are flagged"
+    # continuous random logits carry no exact ties at the benchmark's router shape
+    big = torch.randn(4096, 128, generator=g)
+    assert not O.topk_ties(big, torch.zeros(4096, 8, dtype=torch.long)).any()
+
+
+# ------------------------------------------------------------ the CPU baseline
+
+
+def test_reference_step_equals_block_forward_backward():
+    """reference_step (the CPU baseline: F.grouped_mm on existing leaves) gives
+    the block's outputs and gradients, in fp32 and, at bf16's tolerance, in bf16."""
+    w = WORKLOADS["c1"]
+    inp = {k: v.float() for k, v in make_block_inputs(w, seed=1234, dtype=torch.bfloat16).items()}
+    ref = O.block_forward_backward(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"],
+                                   inp["d_out"], top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=w.aux_coef)
+    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2e-2)):
+        leaves = O.make_leaves(*(inp[k].to(dtype) for k in ("x", "router_weight", "gate_up_proj", "down_proj")))
+        for _ in range(2):  # a second step on the same leaves starts from cleared gradients
+            out = O.reference_step(leaves, inp["d_out"], top_k=w.top_k, norm_topk_prob=w.norm_topk_prob,
+                                   aux_coef=w.aux_coef, compute_dtype=dtype)
+        pairs = [("out", out, ref["out"])] + [(n, l.grad, ref[n]) for n, l in
+                                              zip(("dx", "d_router", "d_gate_up", "d_down"), leaves)]
+        for name, got, want in pairs:
+            err = float((got.float() - want).abs().max() / want.abs().max())
+            assert err <= tol, f"{dtype} {name}: max rel err {err:.2e}"
+
+
+@pytest.mark.parametrize("case", ["small", "c2"])
+def test_aux_loss_masked_branch_matches_transformers_golden(case):
+    """The attention-mask branch over several layers (layer-major logits, the
+    [batch, seq] mask expanded per layer and per top-k slot) against
+    transformers' own load_balancing_loss_func, forward and gradient."""
+    g = np.load(GOLDEN / "aux_masked.npz")
+    layers, batch, seq, E, k, _ = g[f"{case}_meta"].tolist()
+    leaves = [torch.from_numpy(l).clone().requires_grad_() for l in g[f"{case}_logits"]]
+    mask = torch.from_numpy(g[f"{case}_mask"])
+    assert 0 < int((mask == 0).sum()) < mask.numel()
+    aux = O.load_balancing_loss(tuple(leaves), E, k, attention_mask=mask)
+    aux.backward()
+    np.testing.assert_allclose(float(aux), float(g[f"{case}_aux"]), rtol=1e-6)
+    got = np.stack([l.grad.numpy() for l in leaves])
+    np.testing.assert_allclose(got, g[f"{case}_d_logits"], rtol=1e-5, atol=1e-9)
+    unmasked = O.load_balancing_loss(tuple(l.detach() for l in leaves), E, k)
+    np.testing.assert_allclose(float(unmasked), float(g[f"{case}_aux_unmasked"]), rtol=1e-6)
+    # the mask matters: dropping it changes the loss
+    assert abs(float(aux) - float(unmasked)) > 1e-4
