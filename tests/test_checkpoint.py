@@ -40,9 +40,10 @@ def _hub_state(model):
     for name, t in model.state_dict().items():
         if name.endswith("mlp.experts.gate_up_proj"):
             base = name[: -len("gate_up_proj")]
+            half = t.shape[1] // 2  # gate rows first, then up
             for e in range(t.shape[0]):
-                out[f"{base}{e}.gate_proj.weight"] = t[e, :I].contiguous()
-                out[f"{base}{e}.up_proj.weight"] = t[e, I:].contiguous()
+                out[f"{base}{e}.gate_proj.weight"] = t[e, :half].contiguous()
+                out[f"{base}{e}.up_proj.weight"] = t[e, half:].contiguous()
         elif name.endswith("mlp.experts.down_proj"):
             base = name[: -len("down_proj")]
             for e in range(t.shape[0]):
