@@ -190,6 +190,23 @@ int moe_permute_fwd(const void* hidden, int64_t T, int64_t H,
                     int32_t* pos_of_slot, int32_t* counts, int32_t* offsets,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* moe_permute_fwd without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  It has no counterpart in the
+ * reference.  The histogram lives in a fixed 1 MiB device array per GPU
+ * (held until the process ends), so S = T*k routes over num_buckets buckets
+ * must satisfy moe_permute_workspace_bytes(S, num_buckets) <= 1 MiB (about a
+ * million routes at 128 buckets); larger sizes return MOE_ERR_UNSUPPORTED
+ * before any launch.  Calls no hipMalloc or other allocating routine.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, threads or graph replays in flight together) race.
+ * Outputs and semantics are those of moe_permute_fwd, bit for bit. */
+int moe_permute_fwd_noalloc(const void* hidden, int64_t T, int64_t H,
+                            const int64_t* ids, int64_t k, int64_t divisor,
+                            int64_t num_buckets, void* permuted, int32_t* perm,
+                            int32_t* pos_of_slot, int32_t* counts,
+                            int32_t* offsets, void* stream);
+
 /* Per sorted position: local_ids[pos] = ids[perm[pos]] - bucket*divisor and
  * routed_scores[pos] = scores[perm[pos]] (either output may be NULL).
  * Replaces send_experts/send_scores of token_dispatch.py:124-125. */

@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_aux_loss_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _I, _P]),
     "moe_permute_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_permute_fwd": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "moe_permute_fwd_noalloc": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "moe_dispatch_meta": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P]),
     "moe_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),

@@ -1,0 +1,64 @@
+"""The allocation-free routing permutation (moe_permute_fwd_noalloc) against
+moe_permute_fwd, through the C ABI: bit-identical outputs on two calls in a
+row, the second smaller (its fixed scratch keeps the first call's contents),
+and the size limit refused before any launch."""
+
+import ctypes
+
+import pytest
+import torch
+
+from parallel_amd import _lib
+
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _outputs(T, k, nb, H, device):
+    S = T * k
+    i32 = dict(dtype=torch.int32, device=device)
+    return (torch.empty(S, H, dtype=BF, device=device), torch.empty(S, **i32), torch.empty(S, **i32),
+            torch.empty(nb, **i32), torch.empty(nb, **i32))
+
+
+def _run(name, hidden, ids, divisor, nb):
+    T, k = ids.shape
+    H = hidden.shape[1]
+    rows, perm, pos, counts, offsets = _outputs(T, k, nb, H, hidden.device)
+    lib = _lib.load()
+    stream = _lib.stream_of(hidden)
+    common = (hidden.data_ptr(), T, H, ids.data_ptr(), k, divisor, nb, rows.data_ptr(), perm.data_ptr(),
+              pos.data_ptr(), counts.data_ptr(), offsets.data_ptr())
+    if name == "moe_permute_fwd":
+        ws = torch.empty(max(lib.moe_permute_workspace_bytes(T * k, nb), 16), dtype=torch.uint8, device=hidden.device)
+        _lib.check(lib.moe_permute_fwd(*common, ws.data_ptr(), ws.numel(), stream), name)
+    else:
+        _lib.check(lib.moe_permute_fwd_noalloc(*common, stream), name)
+    return rows, perm, pos, counts, offsets
+
+
+@pytest.mark.gpu
+def test_noalloc_permute_equals_permute_on_consecutive_calls():
+    g = torch.Generator().manual_seed(0)
+    cases = [(4096, 8, 1, 128, 2048), (300, 4, 16, 5, 64)]  # (T, k, divisor, buckets, H); the second is smaller
+    for T, k, divisor, nb, H in cases:
+        hidden = torch.randn(T, H, generator=g).to(BF).to(DEV)
+        ids = torch.randint(-2, divisor * (nb + 1), (T, k), generator=g).to(DEV)
+        want = _run("moe_permute_fwd", hidden, ids, divisor, nb)
+        got = _run("moe_permute_fwd_noalloc", hidden, ids, divisor, nb)
+        torch.cuda.synchronize()
+        for label, a, b in zip(("rows", "perm", "pos_of_slot", "counts", "offsets"), got, want):
+            n = int(want[4][-1]) if label == "rows" else None  # sentinel rows are written as zeros by both
+            assert torch.equal(a if n is None else a[:n], b if n is None else b[:n]), f"T={T} {label}"
+        assert not got[0][int(want[4][-1]):].any()
+
+
+def test_noalloc_permute_refuses_sizes_beyond_its_scratch():
+    """Host-side check only: no HIP call happens for a refused size."""
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(64)
+    b = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    # 2**21 routes over 1024 buckets need 4096 chunks x 1025 x 4 bytes > 1 MiB
+    rc = lib.moe_permute_fwd_noalloc(b, 1 << 18, 64, b, 8, 1, 1024, b, b, b, b, b, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED
+    assert b"scratch" in lib.moe_last_error()
