@@ -410,7 +410,7 @@ def main() -> int:
     import torch
 
     sys.path.insert(0, str(ROOT))
-    from parallel_amd import _lib, load_balancing_loss_func, ops
+    from parallel_amd import _lib, ops
     from parallel_amd.workloads import WORKLOADS, make_block_inputs
 
     w = WORKLOADS[args.config]
@@ -448,15 +448,25 @@ def main() -> int:
         d_out = inp["d_out"]
         bias = inp.get("logit_bias")
         coef = torch.tensor(w.aux_coef, device=dev)
-        params = (x, rw, gu, dn)
-        log(f"workload {w.name}: T={w.tokens} H={w.hidden} E={w.experts} k={w.top_k} I={w.intermediate}")
+        # C4 accumulates the weight gradients into pre-existing, seeded
+        # gradient buffers (inside the weight-gradient kernel); the other
+        # configs start every step from cleared gradients.
+        accumulate = w.name == "c4"
+        if accumulate:
+            g = torch.Generator(device=dev).manual_seed(3)
+            for p in (rw, gu, dn):
+                p.grad = torch.randn(p.shape, generator=g, device=dev).mul_(1e-3).to(p.dtype)
+        params = (x,) if accumulate else (x, rw, gu, dn)
+        log(f"workload {w.name}: T={w.tokens} H={w.hidden} E={w.experts} k={w.top_k} I={w.intermediate}"
+            + (" (dW accumulated into existing gradients)" if accumulate else ""))
 
         def step():
             for p in params:
                 p.grad = None
-            logits, scores, idx = ops.router_fwd(x, rw, w.top_k, w.norm_topk_prob, bias)
-            out = ops.experts(x, idx, scores, gu, dn)
-            aux = load_balancing_loss_func((logits,), w.experts, w.top_k)
+            # The router's own softmax and top-k also give the Switch aux loss
+            # (TF load_balancing_loss_func recomputes both from the logits).
+            logits, scores, idx, aux, _ = ops.router_aux_fwd(x, rw, w.top_k, w.norm_topk_prob, None, bias)
+            out = ops.experts(x, idx, scores, gu, dn, accumulate_grad=accumulate)
             torch.autograd.backward([out, aux], [d_out, coef])
 
     for _ in range(args.warmup):
@@ -558,7 +568,8 @@ def main() -> int:
         "data": "synthetic (seeded normal inputs and weights)",
         "config": {"workload": f"{w.name}: Qwen3-30B-A3B MoE block" if w.name in ("c2", "c4") else w.name,
                    "tokens": w.tokens, "hidden": w.hidden, "experts": w.experts, "top_k": w.top_k,
-                   "moe_intermediate": w.intermediate, "router_logits": "fp32", "aux_coef": w.aux_coef},
+                   "moe_intermediate": w.intermediate, "router_logits": "fp32", "aux_coef": w.aux_coef,
+                   "dW": "accumulated into existing gradients" if w.name == "c4" else "written"},
         "grouped_gemm": {"flops_fwd_bwd": gemm_flops, "time_ms": round(gemm_s * 1e3, 4),
                          "tflops": round(gemm_tflops, 1) if gemm_tflops else None,
                          "mfma_frac": round(gemm_tflops / MFMA_BF16_PEAK_TFLOPS, 4) if gemm_tflops else None},
