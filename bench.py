@@ -463,10 +463,12 @@ def main() -> int:
         def step():
             for p in params:
                 p.grad = None
-            # The router's own softmax and top-k also give the Switch aux loss
-            # (TF load_balancing_loss_func recomputes both from the logits).
-            logits, scores, idx, aux, _ = ops.router_aux_fwd(x, rw, w.top_k, w.norm_topk_prob, None, bias)
-            out = ops.experts(x, idx, scores, gu, dn, accumulate_grad=accumulate)
+            # Router, aux loss and experts as one op: the router's own softmax
+            # and top-k also give the Switch aux loss (TF load_balancing_loss_func
+            # recomputes both from the logits), and the backward adds the
+            # router's input gradient to the experts' inside the permute
+            # backward instead of a separate elementwise add.
+            out, _, _, _, aux = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob, None, bias, accumulate)
             torch.autograd.backward([out, aux], [d_out, coef])
 
     for _ in range(args.warmup):

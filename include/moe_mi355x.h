@@ -100,14 +100,32 @@ int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices,
                              int norm_topk_prob, void* d_logits_bf16,
                              void* stream);
 
+/* moe_router_topk_bwd_bf16 with the aux loss's logits gradient (that of
+ * moe_aux_loss_bwd for token_weight, stats and d_aux[1], which are what
+ * moe_router_aux_fwd returned and the loss's incoming gradient) computed in
+ * the same pass: d_logits_bf16 = bf16(g + (d_add + aux term)), bit for bit
+ * moe_aux_loss_bwd's f32 output passed as d_add (added after the caller's
+ * d_add, which may be NULL).  Autograd of modeling_qwen3_moe.py:261-265 and
+ * of load_balancing_loss_func (:514-593) at the router logits. */
+int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indices,
+                            const float* d_scores, const float* d_add,
+                            const float* token_weight, const float* stats,
+                            const float* d_aux, int64_t T, int64_t E,
+                            int64_t k, int norm_topk_prob, void* d_logits_bf16,
+                            void* stream);
+
 /* Backward of the router GEMM (F.linear, modeling_qwen3_moe.py:260) from
  * bf16 d_logits[T,E]: dx[T,H] = d_logits · wr (bf16) and dwr[E,H] =
- * d_logitsᵀ · x (bf16, reduced in f32 over row chunks held in the workspace). */
+ * d_logitsᵀ · x (bf16, reduced in f32 over row chunks held in the workspace).
+ * With dwr_accumulate, dwr holds an existing bf16 gradient and receives
+ * bf16(dwr + bf16(d_logitsᵀ · x)), torch's accumulation of the fresh gradient
+ * (parallel/parallel/engine/engine.py:165-178). */
 size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
 int moe_router_logits_bwd(const void* d_logits_bf16, const void* x,
-                          const void* wr, void* dx, void* dwr, int64_t T,
-                          int64_t H, int64_t E, void* workspace,
-                          size_t workspace_bytes, void* stream);
+                          const void* wr, void* dx, void* dwr,
+                          int dwr_accumulate, int64_t T, int64_t H, int64_t E,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /* ---------------------------------------------------------------- aux loss */
 

@@ -169,31 +169,45 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(const int
   }
 }
 
-// permuted[pos] = hidden[perm[pos] / k] for pos < n_valid, zero after.
-__global__ __launch_bounds__(kPermThreads) void gather_rows_kernel(const bf16_t* __restrict__ hidden, int H,
-                                                                    const int32_t* __restrict__ perm, int S, int k,
-                                                                    const int32_t* __restrict__ n_valid_ptr,
-                                                                    bf16_t* __restrict__ out) {
+// permuted[pos_of_slot[t k + j]] = hidden[t] for the token's slots that sort
+// below n_valid, and zeros for its sentinel slots.  pos_of_slot is a
+// permutation of [0, S), so every row of permuted is written (rows from
+// n_valid on are the sentinels' zeros).  One wave per token reads its row
+// once and writes it k times; a gather over perm would read it once per route.
+template <int KT>
+__global__ __launch_bounds__(kPermThreads) void scatter_rows_kernel(const bf16_t* __restrict__ hidden, int H,
+                                                                     const int32_t* __restrict__ pos_of_slot, int T,
+                                                                     int S, int k,
+                                                                     const int32_t* __restrict__ n_valid_ptr,
+                                                                     bf16_t* __restrict__ out) {
+  constexpr int KM = KT ? KT : kMaxSlots;
   const int lane = threadIdx.x & (kWave - 1);
   const int n_valid = *n_valid_ptr;
   const int nchunk = H / 8;
-  for (int pos = blockIdx.x * (kPermThreads / kWave) + (threadIdx.x >> 6); pos < S;
-       pos += gridDim.x * (kPermThreads / kWave)) {
-    uint4* dst = reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos) * H);
-    if (pos < n_valid) {
-      const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<int64_t>(perm[pos] / k) * H);
-      // Four 16-byte chunks per lane in flight before their stores.
-      int c = lane;
-      for (; c + 3 * kWave < nchunk; c += 4 * kWave) {
-        uint4 v[4];
+  for (int t = blockIdx.x * (kPermThreads / kWave) + (threadIdx.x >> 6); t < T;
+       t += gridDim.x * (kPermThreads / kWave)) {
+    int pos[KM];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = src[c + u * kWave];
+    for (int j = 0; j < KM; ++j) {
+      const bool live = KT ? true : j < k;
+      pos[j] = __builtin_amdgcn_readfirstlane(live ? pos_of_slot[static_cast<int64_t>(t) * k + j] : -1);
+    }
+    const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<int64_t>(t) * H);
+    // Up to four 16-byte chunks per lane in flight before their stores.
+    for (int c0 = lane; c0 < nchunk; c0 += 4 * kWave) {
+      uint4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) dst[c + u * kWave] = v[u];
+      for (int u = 0; u < 4; ++u) v[u] = c0 + u * kWave < nchunk ? src[c0 + u * kWave] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        const int p = pos[j];
+        if (p >= 0 && p < S) {  // (always, for a permutation; a wave-uniform guard)
+          uint4* dst = reinterpret_cast<uint4*>(out + static_cast<int64_t>(p) * H);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (c0 + u * kWave < nchunk) dst[c0 + u * kWave] = p < n_valid ? v[u] : make_uint4(0, 0, 0, 0);
+        }
       }
-      for (; c < nchunk; c += kWave) dst[c] = src[c];
-    } else {
-      for (int c = lane; c < nchunk; c += kWave) dst[c] = make_uint4(0, 0, 0, 0);
     }
   }
 }
@@ -326,10 +340,10 @@ int permute_fwd_run(const void* hidden, int64_t T, int64_t H, const int64_t* ids
   rc = launch_status("moe_permute_fwd(scatter)");
   if (rc) return rc;
   if (permuted) {
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(row_grid(S)), dim3(kPermThreads), 0, st,
-                       static_cast<const bf16_t*>(hidden), static_cast<int>(H), perm, S, static_cast<int>(k),
-                       offsets + (nb - 1), static_cast<bf16_t*>(permuted));
-    rc = launch_status("moe_permute_fwd(gather)");
+    MOE_DISPATCH_K(k, scatter_rows_kernel, dim3(row_grid(T)), dim3(kPermThreads), 0, st,
+                   static_cast<const bf16_t*>(hidden), static_cast<int>(H), pos_of_slot, static_cast<int>(T),
+                   static_cast<int>(S), static_cast<int>(k), offsets + (nb - 1), static_cast<bf16_t*>(permuted));
+    rc = launch_status("moe_permute_fwd(rows)");
   }
   return rc;
 }

@@ -203,6 +203,52 @@ __device__ __forceinline__ void aux_block_partial(float (*part)[2 * LPT * NPL + 
   }
 }
 
+// One token's routing from its raw logits v (the lane's experts sub + j LPT;
+// entries past E are ignored): adds the bias, writes the logits, the top-k
+// softmax scores and indices and, with_aux, the token's aux terms (the
+// arithmetic of aux_partial_kernel's per-slot sums, which start from zero).
+template <int LPT, int NPL, int KT>
+__device__ __forceinline__ void route_token(float (&v)[NPL], int64_t t, int E, int k, int norm,
+                                            const float* __restrict__ bias, float* __restrict__ logits,
+                                            float* __restrict__ scores, int64_t* __restrict__ indices,
+                                            const float* __restrict__ token_weight, bool with_aux, float (&P)[NPL],
+                                            float (&C)[NPL], float& W) {
+  constexpr int KM = KT ? KT : kMaxTopK;
+  const int sub = Tok<LPT>::sub();
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = sub + j * LPT;
+    if (e < E) {
+      if (bias) v[j] += bias[e];
+      logits[t * E + e] = v[j];
+    } else {
+      v[j] = -INFINITY;
+    }
+  }
+  const SoftmaxStats st = softmax_stats<LPT>(v);
+  int sel[KM];
+  float sl[KM];
+  select_topk<LPT>(v, E, k, sel, sl);
+  write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t);
+  if (with_aux) {
+    const float w = token_weight ? token_weight[t] : 1.0f;
+    W = 0.0f + w;
+    const float inv_sum = 1.0f / st.sum;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int e = sub + j * LPT;
+      if (e < E) {
+        P[j] = 0.0f + w * (expf(v[j] - st.max) * inv_sum);
+        float cnt = 0.0f;
+#pragma unroll
+        for (int r = 0; r < KM; ++r)
+          if (r < k && sel[r] == e) cnt += 1.0f;
+        C[j] = 0.0f + w * cnt;
+      }
+    }
+  }
+}
+
 // logits[t] = sum_s partials[s][t] (+ bias), then the top-k softmax of that row.
 // With aux_ws, also the aux-loss partials of the block's tokens from the
 // same softmax and selection (the layout and arithmetic of aux_partial_kernel).
@@ -211,7 +257,6 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
     const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
     float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k_rt, int norm,
     const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
-  constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
   __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];  // E <= LPT NPL
   const int sub = Tok<LPT>::sub();
@@ -250,52 +295,148 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
         v[j] += e < E ? partials[sp * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
       }
     }
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const int e = sub + j * LPT;
-      if (e < E) {
-        if (bias) v[j] += bias[e];
-        logits[static_cast<int64_t>(t) * E + e] = v[j];
-      } else {
-        v[j] = -INFINITY;
-      }
-    }
-    const SoftmaxStats st = softmax_stats<LPT>(v);
-    int sel[KM];
-    float sl[KM];
-    select_topk<LPT>(v, E, k, sel, sl);
-    write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t);
-    if (aux_ws) {
-      const float w = token_weight ? token_weight[t] : 1.0f;
-      // aux_partial_kernel's per-slot sums start from zero: 0 + term.
-      W = 0.0f + w;
-      const float inv_sum = 1.0f / st.sum;
-#pragma unroll
-      for (int j = 0; j < NPL; ++j) {
-        const int e = sub + j * LPT;
-        if (e < E) {
-          P[j] = 0.0f + w * (expf(v[j] - st.max) * inv_sum);
-          float cnt = 0.0f;
-#pragma unroll
-          for (int r = 0; r < KM; ++r)
-            if (r < k && sel[r] == e) cnt += 1.0f;
-          C[j] = 0.0f + w * cnt;
-        }
-      }
-    }
+    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, scores, indices, token_weight, aux_ws != nullptr, P,
+                              C, W);
   }  // t < T
   if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
 
-// out[i] = bf16(sum_c partials[c][i]) over n elements, fixed order.
+// The router GEMM, reduction, top-k softmax and aux partials in one pass, for
+// E <= 256 experts with E a multiple of 16.  A block takes the 16 tokens of
+// the 16-lane token layout (4 waves x 4 tokens).  Their logits
+// x[16 tokens, H] . wr[E, H]^T run on v_mfma_f32_16x16x32_bf16 (A: the token
+// rows, B: 16 experts; lane l holds row l % 16, k 8 (l / 16) .. + 7 of a
+// 32-deep k-step, and D row 4 (l / 16) + i, column l % 16), operands loaded
+// straight from memory: the block's x rows once, wr from L2.  Wave w sums
+// the k-steps w, w + 4, ...; the four wave partials are added in wave order
+// through LDS, and each token then goes through route_token as in
+// router_reduce_topk_kernel.  No split-K partials reach memory.
+constexpr int kFusedTokens = 16;
+
+template <int NPL, int KT>
+__global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
+    float* __restrict__ logits, float* __restrict__ scores, int64_t* __restrict__ indices, int T, int H, int E,
+    int k_rt, int norm, const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
+  constexpr int LPT = 16;
+  constexpr int NE = NPL;          // 16-expert tiles covered (E <= 16 NPL)
+  constexpr int ROW = 16 * NE + 4;  // padded LDS row: the four 4-token row groups of a tile hit distinct banks
+  static_assert(Tok<LPT>::kPerBlock == kFusedTokens, "a block's token slots are the MFMA tile's 16 rows");
+  const int k = KT ? KT : k_rt;
+  __shared__ float wpart[kRouterWaves][kFusedTokens][ROW];
+  __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * kFusedTokens;
+  const int ne = E / 16;
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  f32x4_t acc[NE];
+#pragma unroll
+  for (int n = 0; n < NE; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // Operands come through buffer resources: an offset past a resource's end
+  // reads zeros, so rows past T or E and k past H need no branches, and the
+  // offsets are 32-bit.  A ring of D k-steps of operands sits in registers;
+  // a k-step's slot is refilled with the k-step D ahead right after its
+  // MFMAs are issued.
+  constexpr uint32_t kOut = 0x80000000u;  // >= both resource sizes (checked on the host)
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(x), 0, static_cast<int>(static_cast<uint32_t>(T) * H * 2u),
+                                        0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(wr), 0, static_cast<int>(static_cast<uint32_t>(E) * H * 2u),
+                                        0x00020000);
+  const int nks = (H + 31) / 32;
+  const bool t_ok = t0 + r16 < T;
+  const uint32_t xrow = static_cast<uint32_t>(t0 + r16) * static_cast<uint32_t>(H) * 2u;
+  const uint32_t wrow = static_cast<uint32_t>(r16) * static_cast<uint32_t>(H) * 2u;
+  const uint32_t wtile = 16u * static_cast<uint32_t>(H) * 2u;  // bytes between 16-expert tiles
+  // x comes from HBM once, so a wave loads its x fragments for XC k-steps
+  // at once (one memory round trip per chunk); wr, read by every block, comes
+  // from L2 through a ring of D k-steps, refilled D ahead.  Within a chunk the
+  // code is straight-line, so the waits count exactly.
+  constexpr int XC = 16;               // k-steps per wave per chunk
+  constexpr int D = NE <= 8 ? 4 : 2;   // wr ring depth
+  static_assert(XC % D == 0, "the ring turns over whole chunks");
+  auto load16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) __attribute__((always_inline)) {
+    typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+    const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  };
+  auto kbytes = [&](int ks, bool& ok) __attribute__((always_inline)) {
+    const int kk = ks * 32 + kq;
+    ok = kk < H;  // H % 8 == 0: a lane's 8 k are all inside or all outside
+    return static_cast<uint32_t>(kk) * 2u;
+  };
+  uint4 rb[D][NE];
+  auto fetch_w = [&](int ks, uint4 (&b)[NE]) __attribute__((always_inline)) {
+    bool ok;
+    const uint32_t kb = kbytes(ks, ok);
+#pragma unroll
+    for (int n = 0; n < NE; ++n)
+      b[n] = load16(rw, (n < ne && ok) ? wrow + static_cast<uint32_t>(n) * wtile + kb : kOut);
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) fetch_w(wave + kRouterWaves * d, rb[d]);
+  for (int c0 = wave; c0 < nks; c0 += kRouterWaves * XC) {
+    uint4 xa[XC];
+#pragma unroll
+    for (int q = 0; q < XC; ++q) {
+      bool ok;
+      const uint32_t kb = kbytes(c0 + kRouterWaves * q, ok);
+      xa[q] = load16(rx, (t_ok && ok) ? xrow + kb : kOut);
+    }
+#pragma unroll
+    for (int q = 0; q < XC; ++q) {
+      const int d = q % D;
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa[q]);
+      // (tiles past E multiply the zeros their loads read)
+#pragma unroll
+      for (int n = 0; n < NE; ++n)
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, rb[d][n]), acc[n], 0, 0, 0);
+      fetch_w(c0 + kRouterWaves * (q + D), rb[d]);
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NE; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wpart[wave][4 * (lane >> 4) + i][16 * n + r16] = acc[n][i];
+  __syncthreads();
+  const int sub = Tok<LPT>::sub(), slot = Tok<LPT>::slot();
+  const int t = t0 + slot;
+  float P[NPL], C[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
+  float W = 0.0f;
+  if (t < T) {
+    float v[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int e = sub + j * LPT;
+      v[j] = ((wpart[0][slot][e] + wpart[1][slot][e]) + wpart[2][slot][e]) + wpart[3][slot][e];
+    }
+    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, scores, indices, token_weight, aux_ws != nullptr, P,
+                              C, W);
+  }
+  if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
+}
+
+// out[i] = bf16(sum_c partials[c][i]) over n elements, fixed order; with
+// accumulate, out[i] = bf16(out[i] + bf16(sum)), torch's bf16 add of a fresh
+// gradient into an existing one.
 __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, int chunks, int64_t n,
-                                            bf16_t* __restrict__ out) {
+                                            bf16_t* __restrict__ out, int accumulate) {
   for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x * 4) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int c = 0; c < chunks; ++c) {
       float4 v = *reinterpret_cast<const float4*>(partials + c * n + i);
       acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    if (accumulate) {
+      const uint2 old = *reinterpret_cast<const uint2*>(out + i);
+      acc.x = bf16_to_f32(f32_to_bf16(acc.x)) + lo_bf16(old.x);
+      acc.y = bf16_to_f32(f32_to_bf16(acc.y)) + hi_bf16(old.x);
+      acc.z = bf16_to_f32(f32_to_bf16(acc.z)) + lo_bf16(old.y);
+      acc.w = bf16_to_f32(f32_to_bf16(acc.w)) + hi_bf16(old.y);
     }
     uint2 o;
     o.x = pack_bf16x2(acc.x, acc.y);
@@ -306,11 +447,16 @@ __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, 
 
 // d_logits = p * (dp - <dp, p>) (+ d_add), dp scattered from the (renormalised)
 // top-k; the f32 result goes to d_logits and its bf16 rounding to
-// d_logits_bf16 (either may be null).  d_add may alias d_logits.
+// d_logits_bf16 (either may be null).  d_add may alias d_logits.  With
+// aux_stats, the aux loss's logits gradient is added as well, computed as
+// aux_bwd_kernel computes it (from the same softmax) and added where d_add
+// would be: the result is the bits of aux_bwd_kernel's output passed as
+// d_add.
 template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ indices, const float* __restrict__ d_scores, int T,
-    int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16) {
+    int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16,
+    const float* __restrict__ token_weight, const float* __restrict__ aux_stats, const float* __restrict__ d_aux) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
   const int sub = Tok<LPT>::sub();
@@ -329,6 +475,31 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
   }
   const SoftmaxStats st = softmax_stats<LPT>(v);
   const float inv_sum = 1.0f / st.sum;
+  if (aux_stats) {
+    // aux_bwd_kernel's term: p_e (g_e - <g, p>), g_e = d_aux E w c_e / W^2.
+    const float W = aux_stats[E];
+    const float w = token_weight ? token_weight[t] : 1.0f;
+    const float scale = d_aux[0] * static_cast<float>(E) * w / (W * W);
+    float p[NPL], g[NPL];
+    float dot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int e = sub + j * LPT;
+      p[j] = 0.0f;
+      g[j] = 0.0f;
+      if (e < E) {
+        p[j] = expf(v[j] - st.max) * inv_sum;
+        g[j] = scale * aux_stats[e];
+        dot += p[j] * g[j];
+      }
+    }
+    dot = tok_sum<LPT>(dot);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const float d = p[j] * (g[j] - dot);
+      add[j] = d_add ? add[j] + d : d;
+    }
+  }
 
   int idx[KM];
   float pv[KM], ds[KM];
@@ -374,7 +545,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
         if (r < k && idx[r] == e) dp += dv[r];
       float p = expf(v[j] - st.max) * inv_sum;
       float g = p * (dp - c);
-      if (d_add) g += add[j];
+      if (d_add || aux_stats) g += add[j];
       if (d_logits) d_logits[base + e] = g;
       if (d_logits_bf16) d_logits_bf16[base + e] = f32_to_bf16(g);
     }
@@ -493,6 +664,19 @@ __global__ __launch_bounds__(1024) void aux_finalize_kernel(const float* __restr
   }
   if (tid == 0) aux[0] = static_cast<float>(E) * terms[0];
 }
+
+namespace {
+// The aux loss from per-block partial rows: the row-group sums, then the loss.
+int aux_reduce_finalize(float* ws, int nblk, int64_t E, float* stats, float* aux, hipStream_t st, const char* name) {
+  const int n = static_cast<int>(2 * E + 1);
+  float* sums = ws + static_cast<int64_t>(nblk) * n;
+  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64, kAuxGroups), dim3(256), 0, st, ws, nblk, n, sums);
+  int rc = launch_status(name);
+  if (rc) return rc;
+  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, st, sums, static_cast<int>(E), stats, aux);
+  return launch_status(name);
+}
+}  // namespace
 
 template <int LPT, int NPL>
 __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const float* __restrict__ logits,
@@ -623,7 +807,8 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
                        dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       accumulate ? d_logits : nullptr, d_logits, static_cast<bf16_t*>(d_logits_bf16));
+                       accumulate ? d_logits : nullptr, d_logits, static_cast<bf16_t*>(d_logits_bf16), nullptr,
+                       nullptr, nullptr);
   });
   return launch_status("moe_router_topk_bwd");
 }
@@ -641,9 +826,29 @@ extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indi
                        dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16));
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), nullptr, nullptr, nullptr);
   });
   return launch_status("moe_router_topk_bwd_bf16");
+}
+
+extern "C" int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
+                                       const float* d_add, const float* token_weight, const float* stats,
+                                       const float* d_aux, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                                       void* d_logits_bf16, void* stream) {
+  int rc = check_router(T, E, k);
+  if (rc) return rc;
+  if (T == 0) return MOE_OK;
+  MOE_REQUIRE(logits && indices && d_scores && stats && d_aux && d_logits_bf16, MOE_ERR_INVALID,
+              "router aux bwd bf16: null pointer");
+  int blocks = token_blocks(T, E, true);
+  with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks),
+                       dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), token_weight, stats, d_aux);
+  });
+  return launch_status("moe_router_aux_bwd_bf16");
 }
 
 extern "C" size_t moe_aux_loss_workspace_bytes(int64_t T, int64_t E) {
@@ -669,15 +874,7 @@ extern "C" int moe_aux_loss_fwd(const float* logits, const float* token_weight, 
   });
   rc = launch_status("moe_aux_loss_fwd(partial)");
   if (rc) return rc;
-  const int n = static_cast<int>(2 * E + 1);
-  float* sums = ws + static_cast<int64_t>(nblk) * n;
-  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64, kAuxGroups), dim3(256), 0, as_stream(stream), ws, nblk,
-                     n, sums);
-  rc = launch_status("moe_aux_loss_fwd(reduce)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, as_stream(stream), sums, static_cast<int>(E), stats,
-                     aux);
-  return launch_status("moe_aux_loss_fwd(finalize)");
+  return aux_reduce_finalize(ws, nblk, E, stats, aux, as_stream(stream), "moe_aux_loss_fwd(reduce)");
 }
 
 extern "C" int moe_aux_loss_bwd(const float* logits, const float* token_weight, const float* stats, const float* d_aux,
@@ -713,8 +910,47 @@ void router_split(int64_t T, int64_t H, int64_t E, int& splits, int& k_chunk) {
 }
 }  // namespace
 
+namespace {
+// The one-pass router kernel covers up to 256 experts in 16-expert MFMA
+// tiles, with x and wr each under 2 GiB (its buffer resources).
+bool router_fused(int64_t T, int64_t H, int64_t E) {
+  constexpr int64_t kMax = (1ll << 31) - 64;
+  return E <= 256 && E % 16 == 0 && T * H * 2 < kMax && E * H * 2 < kMax;
+}
+
+// logits, scores and indices of T >= 1 tokens and, with aux_ws, the aux
+// partials of token_blocks(T, E) blocks; `partials` is the split-K workspace
+// of the two-pass path (other expert counts).
+int route_tokens(const void* x, const void* wr, const float* bias, float* logits, float* scores, int64_t* indices,
+                 int64_t T, int64_t H, int64_t E, int64_t k, int norm, const float* token_weight, float* aux_ws,
+                 float* partials, hipStream_t st, const char* name) {
+  const int blocks = token_blocks(T, E);
+  if (router_fused(T, H, E)) {
+    with_npl_k(E, k, [&](auto, auto N, auto K) {
+      hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                         dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
+                         static_cast<const bf16_t*>(wr), bias, logits, scores, indices, static_cast<int>(T),
+                         static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm, token_weight, aux_ws);
+    });
+    return launch_status(name);
+  }
+  int splits, k_chunk;
+  router_split(T, H, E, splits, k_chunk);
+  int rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
+                                  static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
+  if (rc) return rc;
+  with_npl_k(E, k, [&](auto L, auto N, auto K) {
+    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
+                       dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits, bias, logits, scores,
+                       indices, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm, token_weight,
+                       aux_ws);
+  });
+  return launch_status(name);
+}
+}  // namespace
+
 extern "C" size_t moe_router_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
-  if (T < 0 || H < 1 || E < 1) return 0;
+  if (T < 0 || H < 1 || E < 1 || router_fused(T, H, E)) return 0;
   int splits, k_chunk;
   router_split(T, H, E, splits, k_chunk);
   return static_cast<size_t>(splits) * static_cast<size_t>(T) * static_cast<size_t>(E) * sizeof(float);
@@ -731,24 +967,10 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
               (long long)H, (long long)E);
   if (T == 0) return MOE_OK;  // no tokens: empty buffers may be NULL
   const size_t need = moe_router_fwd_workspace_bytes(T, H, E);
-  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "router fwd: workspace %zu < %zu bytes",
-              workspace_bytes, need);
-  int splits, k_chunk;
-  router_split(T, H, E, splits, k_chunk);
-  float* partials = static_cast<float*>(workspace);
-  hipStream_t st = as_stream(stream);
-  rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
-                              static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
-  if (rc) return rc;
-  int blocks = token_blocks(T, E);
-  with_npl_k(E, k, [&](auto L, auto N, auto K) {
-    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
-                       dim3(blocks),
-                       dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
-                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       nullptr, nullptr);
-  });
-  return launch_status("moe_router_fwd(reduce+topk)");
+  MOE_REQUIRE((workspace || need == 0) && workspace_bytes >= need, MOE_ERR_WORKSPACE,
+              "router fwd: workspace %zu < %zu bytes", workspace_bytes, need);
+  return route_tokens(x, wr, logit_bias, logits, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0, nullptr,
+                      nullptr, static_cast<float*>(workspace), as_stream(stream), "moe_router_fwd");
 }
 
 extern "C" size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
@@ -773,31 +995,13 @@ extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* lo
   const size_t need = moe_router_aux_fwd_workspace_bytes(T, H, E);
   MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE, "router aux fwd: workspace %zu < %zu bytes",
               workspace_bytes, need);
-  int splits, k_chunk;
-  router_split(T, H, E, splits, k_chunk);
   float* partials = static_cast<float*>(workspace);
   float* aux_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + moe_router_fwd_workspace_bytes(T, H, E));
   hipStream_t st = as_stream(stream);
-  rc = router_logits_partials(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), partials,
-                              static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), splits, k_chunk, st);
+  rc = route_tokens(x, wr, logit_bias, logits, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0, token_weight,
+                    aux_ws, partials, st, "moe_router_aux_fwd(route)");
   if (rc) return rc;
-  const int blocks = token_blocks(T, E);
-  with_npl_k(E, k, [&](auto L, auto N, auto K) {
-    hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
-                       dim3(blocks),
-                       dim3(kRouterWaves * kWave), 0, st, partials, splits, logit_bias, logits, scores, indices,
-                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       token_weight, aux_ws);
-  });
-  rc = launch_status("moe_router_aux_fwd(reduce+topk+aux partials)");
-  if (rc) return rc;
-  const int n = static_cast<int>(2 * E + 1);
-  float* sums = aux_ws + static_cast<int64_t>(blocks) * n;
-  hipLaunchKernelGGL(aux_reduce_kernel, dim3((n + 63) / 64, kAuxGroups), dim3(256), 0, st, aux_ws, blocks, n, sums);
-  rc = launch_status("moe_router_aux_fwd(reduce)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(aux_finalize_kernel, dim3(1), dim3(1024), 0, st, sums, static_cast<int>(E), stats, aux);
-  return launch_status("moe_router_aux_fwd(finalize)");
+  return aux_reduce_finalize(aux_ws, token_blocks(T, E), E, stats, aux, st, "moe_router_aux_fwd(reduce)");
 }
 
 extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
@@ -808,9 +1012,10 @@ extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, in
 }
 
 extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, const void* wr, void* dx, void* dwr,
-                                     int64_t T, int64_t H, int64_t E, void* workspace, size_t workspace_bytes,
-                                     void* stream) {
-  // With no tokens only dWr (zeros) is written; the empty buffers may be NULL.
+                                     int dwr_accumulate, int64_t T, int64_t H, int64_t E, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  // With no tokens only dWr (zeros, or unchanged when accumulating) is
+  // written; the empty buffers may be NULL.
   MOE_REQUIRE(wr && dwr && (T == 0 || (d_logits_bf16 && x && dx)), MOE_ERR_INVALID,
               "router logits bwd: null pointer");
   MOE_REQUIRE(T >= 0 && H > 0 && E > 0 && H % 8 == 0 && E % 8 == 0, MOE_ERR_UNSUPPORTED,
@@ -836,6 +1041,6 @@ extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, c
   int blocks = static_cast<int>((n / 4 + 255) / 256);
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(reduce_partials_bf16_kernel, dim3(blocks), dim3(256), 0, st, partials, chunks, n,
-                     static_cast<bf16_t*>(dwr));
+                     static_cast<bf16_t*>(dwr), dwr_accumulate ? 1 : 0);
   return launch_status("moe_router_logits_bwd(reduce)");
 }

@@ -14,6 +14,7 @@ Ops (namespace ``parallel_amd``):
   combine_rows_fwd / _bwd          gather-form index_add back to source tokens
   rmsnorm_fwd / rmsnorm_bwd        post_attention_layernorm of the block input (+ backward)
   router_aux_fwd                   router_fwd plus the aux loss from the same top-k
+  moe_block_fwd                    router, aux loss and experts as one op (moe_block)
 
 experts_bwd_kernels issues the expert backward's launches with a caller-chosen
 weight-gradient target (fsdp_bucket uses it to write into an FSDP bucket).
@@ -114,10 +115,17 @@ def _(x, weight, top_k, norm_topk_prob, logit_bias=None):
             x.new_empty(T, top_k, dtype=torch.int64))
 
 
-@torch.library.custom_op(f"{LIB}::router_bwd", mutates_args=())
-def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
-               d_scores: Tensor | None, norm_topk_prob: bool) -> tuple[Tensor, Tensor]:
-    """(dx [T,H] bf16, dweight [E,H] bf16) through top-k/renorm/softmax and the router GEMM."""
+def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
+                       d_scores: Tensor | None, norm_topk_prob: bool, token_weight: Tensor | None = None,
+                       stats: Tensor | None = None, d_aux: Tensor | None = None,
+                       dw_target: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
+    """The router backward's launches: (dx [T,H] bf16, dweight [E,H] bf16).
+
+    d_logits is the logits' incoming gradient (fp32, may be None); with
+    ``d_aux`` (and the ``stats``/``token_weight`` of router_aux_fwd) the aux
+    loss's logits gradient is added in the same top-k backward pass.  With
+    ``dw_target`` (the router weight's existing bf16 gradient) the weight
+    gradient is added into it and None is returned in its place."""
     x = x.contiguous()
     weight = weight.contiguous()
     T, H = x.shape
@@ -131,14 +139,27 @@ def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_log
     d_scores = d_scores.float().contiguous()
     # Only the bf16 d_logits feeds the GEMMs; the incoming logits gradient is
     # read, not copied.
-    call("moe_router_topk_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
-         int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
+    if d_aux is not None:
+        tw = None if token_weight is None else token_weight.float().contiguous()
+        da = d_aux.float().reshape(1).contiguous()
+        call("moe_router_aux_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), ptr(tw), ptr(stats),
+             ptr(da), T, E, k, int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
+    else:
+        call("moe_router_topk_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
+             int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
     dx = torch.empty(T, H, dtype=BF16, device=x.device)
-    dw = torch.empty(E, H, dtype=weight.dtype, device=x.device)
+    dw = dw_target if dw_target is not None else torch.empty(E, H, dtype=weight.dtype, device=x.device)
     ws = _ws(_lib.load().moe_router_logits_bwd_workspace_bytes(T, H, E), x.device)
-    call("moe_router_logits_bwd", ptr(dl_bf16), ptr(x), ptr(weight), ptr(dx), ptr(dw), T, H, E, ptr(ws), ws.numel(),
-         s, tag="router_gemm_bwd")
-    return dx, dw
+    call("moe_router_logits_bwd", ptr(dl_bf16), ptr(x), ptr(weight), ptr(dx), ptr(dw), int(dw_target is not None),
+         T, H, E, ptr(ws), ws.numel(), s, tag="router_gemm_bwd")
+    return dx, (None if dw_target is not None else dw)
+
+
+@torch.library.custom_op(f"{LIB}::router_bwd", mutates_args=())
+def router_bwd(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
+               d_scores: Tensor | None, norm_topk_prob: bool) -> tuple[Tensor, Tensor]:
+    """(dx [T,H] bf16, dweight [E,H] bf16) through top-k/renorm/softmax and the router GEMM."""
+    return router_bwd_kernels(x, weight, logits, indices, d_logits, d_scores, norm_topk_prob)
 
 
 @router_bwd.register_fake
@@ -292,6 +313,10 @@ def router_aux_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool, 
                    logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """router_fwd plus the Switch aux loss from the same softmax and top-k: (logits, scores, indices,
     aux scalar, stats [E+1]); aux equals aux_loss_fwd(logits, token_weight, E, top_k)."""
+    return _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias)
+
+
+def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias):
     _require_gpu(x, weight, token_weight)
     _require_bf16("router input", x)
     _require_bf16("router weight", weight)
@@ -332,11 +357,8 @@ def _router_aux_setup(ctx, inputs, output):
 
 def _router_aux_backward(ctx, d_logits, d_scores, _d_idx, d_aux, _d_stats):
     x, weight, logits, idx, token_weight, stats = ctx.saved_tensors
-    dl = d_logits
-    if d_aux is not None:
-        dl_aux = aux_loss_bwd(logits, token_weight, stats, d_aux)
-        dl = dl_aux if dl is None else dl.float() + dl_aux
-    dx, dw = router_bwd(x, weight, logits, idx, dl, d_scores, ctx.norm)
+    # The aux loss's logits gradient is formed inside the top-k backward pass.
+    dx, dw = router_bwd_kernels(x, weight, logits, idx, d_logits, d_scores, ctx.norm, token_weight, stats, d_aux)
     return dx, dw, None, None, None, None
 
 
@@ -423,6 +445,10 @@ def experts_fwd(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate
     y [S,H], pos_of_slot [S] int32, offsets [E] int32).  ``accumulate_grad``
     only changes the backward (see ``experts``).
     """
+    return _experts_fwd_kernels(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
+
+
+def _experts_fwd_kernels(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj):
     T, H, k, E, I = _check_experts(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
     S = T * k
     dev = hidden.device
@@ -463,11 +489,14 @@ def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_gr
 
 def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
                         pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor, offsets: Tensor,
-                        wgrad) -> tuple[Tensor, Tensor, object, object]:
+                        wgrad, on_d_weights=None) -> tuple[Tensor, Tensor, object, object]:
     """The expert backward's launches; ``wgrad(name, dc, a, n, k)`` issues the
     weight gradient dW[g][n,k] = dc[rows of g]ᵀ · a[rows of g] of projection
     ``name`` ("gate_up_proj", then "down_proj") and returns whatever stands for
-    it.  Returns (d_hidden [T,H], d_weights [T,k] f32, wgrad's two results)."""
+    it.  ``on_d_weights(d_weights)``, if given, runs as soon as the routing
+    weights' gradient exists and returns a bf16 [T,H] gradient that the
+    permute backward adds into d_hidden (the other path to the same input).
+    Returns (d_hidden [T,H], d_weights [T,k] f32, wgrad's two results)."""
     T, k = top_k_weights.shape
     E, I2, H = gate_up_proj.shape
     I = I2 // 2
@@ -480,6 +509,7 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     d_w = torch.empty(T, k, dtype=torch.float32, device=dev)
     call("moe_combine_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
          ptr(d_w), s, tag="combine_bwd")
+    d_add = on_d_weights(d_w) if on_d_weights is not None else None
     d_pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
     call("moe_grouped_gemm_dgrad_swiglu_bwd", ptr(dy), ptr(down_proj), ptr(pre), ptr(offsets), E, S, H, I,
          ptr(d_pre), s, tag="down_dgrad")
@@ -491,7 +521,7 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     call("moe_grouped_gemm_dgrad", ptr(d_pre), ptr(gate_up_proj), ptr(offsets), E, S, 2 * I, H, ptr(d_xp), s,
          tag="up_dgrad")
     d_hidden = torch.empty(T, H, dtype=BF16, device=dev)
-    call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, None, ptr(d_hidden), s,
+    call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, ptr(d_add), ptr(d_hidden), s,
          tag="permute_bwd")
     d_gu = wgrad("gate_up_proj", d_pre, xp, 2 * I, H)
     d_down = wgrad("down_proj", dy, act, H, I)
@@ -602,6 +632,117 @@ def experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_
     unit waits for those hooks (parallel/parallel/engine/_dp_param_unit.py:669-690).
     A weight without a ``.grad`` gets a fresh gradient as usual."""
     return experts_fwd(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_grad)[0]
+
+
+# --------------------------------------------- the whole block in one op
+
+
+@torch.library.custom_op(f"{LIB}::moe_block_fwd", mutates_args=())
+def moe_block_fwd(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj: Tensor, top_k: int,
+                  norm_topk_prob: bool, token_weight: Tensor | None = None, logit_bias: Tensor | None = None,
+                  accumulate_grad: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                                          Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """router_aux_fwd then experts_fwd on its routes: (out, logits, scores,
+    indices, aux, stats, and experts_fwd's saved tensors)."""
+    logits, scores, idx, aux, stats = _router_aux_kernels(x, router_weight, top_k, norm_topk_prob, token_weight,
+                                                          logit_bias)
+    out, xp, pre, act, y, pos, offsets = _experts_fwd_kernels(x, idx, scores, gate_up_proj, down_proj)
+    return out, logits, scores, idx, aux, stats, xp, pre, act, y, pos, offsets
+
+
+@moe_block_fwd.register_fake
+def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, token_weight=None, logit_bias=None,
+      accumulate_grad=False):
+    T, H = x.shape
+    E = router_weight.shape[0]
+    router = (x.new_empty(T, E, dtype=torch.float32), x.new_empty(T, top_k, dtype=torch.float32),
+              x.new_empty(T, top_k, dtype=torch.int64), x.new_empty((), dtype=torch.float32),
+              x.new_empty(E + 1, dtype=torch.float32))
+    out, xp, pre, act, y, pos, offsets = _experts_fake(x, top_k, gate_up_proj)
+    return (out, *router, xp, pre, act, y, pos, offsets)
+
+
+def _experts_fake(x, top_k, gate_up_proj):
+    T, H = x.shape
+    S = T * top_k
+    E, I2, _ = gate_up_proj.shape
+    i32 = dict(dtype=torch.int32)
+    return (x.new_empty(T, H), x.new_empty(S, H), x.new_empty(S, I2), x.new_empty(S, I2 // 2), x.new_empty(S, H),
+            x.new_empty(S, **i32), x.new_empty(E, **i32))
+
+
+def _block_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
+    x, rw, gu, dn, top_k, norm, token_weight, _bias, accumulate_grad = inputs
+    _, logits, scores, idx, _, stats, xp, pre, act, y, pos, offsets = output
+    ctx.save_for_backward(x, rw, gu, dn, logits, scores, idx, token_weight, stats, xp, pre, act, y, pos, offsets)
+    ctx.norm = norm
+    ctx.x_dtype = x.dtype
+    ctx.params = (rw, gu, dn) if accumulate_grad else None
+    ctx.mark_non_differentiable(idx, stats, xp, pre, act, y, pos, offsets)
+
+
+def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
+    x, rw, gu, dn, logits, scores, idx, tw, stats, xp, pre, act, y, pos, offsets = ctx.saved_tensors
+    if d_out is None and d_logits is None and d_scores is None and d_aux is None:
+        return (None,) * 9
+    targets = [_grad_target(p) for p in ctx.params] if ctx.params is not None else [None, None, None]
+    rw_target = targets[0] if targets[0] is not None and targets[0].dtype == BF16 else None
+    E = gu.shape[0]
+    S = xp.shape[0]
+    s = _stream(x)
+    grads = {}
+
+    def router_backward(d_w):
+        # The routing weights' gradient from the experts plus any the scores
+        # received elsewhere; the router's dX then joins d_hidden inside the
+        # permute backward instead of a separate add.
+        ds = d_w if d_scores is None else d_w + d_scores.float()
+        dx_router, grads["router"] = router_bwd_kernels(x, rw, logits, idx, d_logits, ds, ctx.norm, tw, stats, d_aux,
+                                                        rw_target)
+        return dx_router
+
+    params = {"gate_up_proj": (gu, targets[1]), "down_proj": (dn, targets[2])}
+
+    def wgrad(name, dc, a, n, k):
+        param, target = params[name]
+        tag = "up_wgrad" if name == "gate_up_proj" else "down_wgrad"
+        if target is None:
+            dw = torch.empty_like(param)
+            call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s, tag=tag)
+            return dw
+        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(target),
+             int(target.dtype == torch.float32), 1, s, tag=tag)
+        return None
+
+    if d_out is None:
+        d_out = torch.zeros_like(x)
+    dx, _d_w, d_gu, d_dn = experts_bwd_kernels(d_out, scores, gu, dn, xp, pre, act, y, pos, offsets, wgrad,
+                                              on_d_weights=router_backward)
+    return dx.to(ctx.x_dtype), grads["router"], d_gu, d_dn, None, None, None, None, None
+
+
+moe_block_fwd.register_autograd(_block_backward, setup_context=_block_setup)
+
+
+def moe_block(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj: Tensor, top_k: int,
+              norm_topk_prob: bool, token_weight: Tensor | None = None, logit_bias: Tensor | None = None,
+              accumulate_grad: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Qwen3MoeSparseMoeBlock's router, experts and Switch aux loss as one op:
+    (out [T,H], router_logits [T,E] fp32, scores [T,k], indices [T,k], aux).
+
+    The same results as ``router_aux_fwd`` followed by ``experts`` (TF
+    modeling_qwen3_moe.py:249-267 and integrations/moe.py:377-478, the aux
+    loss of :514-593), but the backward adds the router's input gradient to
+    the experts' inside the permute backward (one rounding of the sum of
+    both in fp32, where autograd rounds the experts' sum, then adds), forms
+    the aux loss's logits gradient inside the top-k backward, and with
+    ``accumulate_grad`` adds every weight gradient into an existing ``.grad``
+    (bf16 router weight; bf16 or fp32 expert weights) in the kernels, as
+    ``experts`` does for the expert weights."""
+    out, logits, scores, idx, aux = moe_block_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
+                                                  token_weight, logit_bias, accumulate_grad)[:5]
+    return out, logits, scores, idx, aux
 
 
 # ------------------------------------------------------- token dispatch ops

@@ -1,0 +1,115 @@
+"""The one-pass router (GEMM, reduction, top-k softmax and aux partials in one
+kernel), the router backward with the aux loss's gradient formed in the same
+pass, and the whole block as one op (``ops.moe_block``), on the GPU.
+
+References: the CPU oracle (router_logits / topk_softmax / block_forward_backward,
+following TF modeling_qwen3_moe.py:249-267, :514-593 and integrations/moe.py:377-478),
+and the separate ops, whose kernels the fused paths share: where the
+arithmetic is the same the results must be the same bits."""
+
+import pytest
+import torch
+
+from conftest import close_bf16, routing_check
+from oracle import moe_oracle as O
+from parallel_amd import ops
+from parallel_amd.workloads import WORKLOADS, make_block_inputs, scaled
+from test_gpu_block import compare, gpu_block_step, oracle_step
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# Every experts-per-lane width of the one-pass kernel (E = 16, 32, 64, 96/128,
+# 256), H with a partial last k-step (72, 136, 264, 520), T not a multiple of
+# the block's 16 tokens; E = 120 takes the split-K path.
+ROUTER_CASES = [(257, 72, 16, 4), (300, 136, 32, 3), (1000, 520, 64, 6), (200, 264, 96, 5), (4096, 2048, 128, 8),
+                (129, 256, 256, 8), (300, 72, 120, 8)]
+
+
+@pytest.mark.parametrize("T,H,E,k", ROUTER_CASES)
+def test_router_aux_fwd_matches_fp32_and_the_standalone_kernels(T, H, E, k):
+    x = torch.randn(T, H, generator=gen(T)).to(BF)
+    w = (torch.randn(E, H, generator=gen(E)) * 0.05).to(BF)
+    bias = torch.randn(E, generator=gen(7)) * 0.3
+    tw = (torch.rand(T, generator=gen(8)) > 0.2).float()
+    logits, scores, idx, aux, stats = ops.router_aux_fwd(x.to(DEV), w.to(DEV), k, True, tw.to(DEV), bias.to(DEV))
+    ref = O.router_logits(x, w) + bias
+    torch.testing.assert_close(logits.cpu(), ref, rtol=1e-4, atol=1e-5)
+    routing_check(idx, O.topk_softmax(ref, k, True)[1], logits)
+    # the routing and the loss are those of the standalone kernels on the returned logits, bit for bit
+    s2, i2 = ops.router_topk(logits, k, True)
+    assert torch.equal(i2, idx) and torch.equal(s2, scores)
+    aux2, stats2 = ops.aux_loss_fwd(logits, tw.to(DEV), E, k)
+    assert torch.equal(aux, aux2) and torch.equal(stats, stats2)
+    ref_aux = O.load_balancing_loss((ref,), E, k, attention_mask=tw.reshape(1, T))
+    torch.testing.assert_close(aux.cpu(), ref_aux, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("T,H,E,k,masked", [(1000, 256, 64, 6, True), (512, 2048, 128, 8, False),
+                                             (300, 72, 120, 8, True)])
+def test_router_aux_backward_is_the_two_pass_gradient_bit_for_bit(T, H, E, k, masked):
+    """The aux loss's logits gradient formed inside the top-k backward gives
+    the bits of moe_aux_loss_bwd's output added by the separate pass."""
+    x = torch.randn(T, H, generator=gen(1)).to(BF).to(DEV)
+    w = (torch.randn(E, H, generator=gen(2)) * 0.05).to(BF).to(DEV)
+    tw = (torch.rand(T, generator=gen(3)) > 0.3).float().to(DEV) if masked else None
+    d_scores = torch.randn(T, k, generator=gen(4)).to(DEV)
+    d_logits = (torch.randn(T, E, generator=gen(5)) * 0.01).to(DEV)
+    d_aux = torch.tensor(0.37, device=DEV)
+    xg, wg = x.clone().requires_grad_(), w.clone().requires_grad_()
+    logits, scores, idx, aux, stats = ops.router_aux_fwd(xg, wg, k, True, tw)
+    torch.autograd.backward([scores, logits, aux], [d_scores, d_logits, d_aux])
+    dl_aux = ops.aux_loss_bwd(logits.detach(), tw, stats, d_aux)
+    dx2, dw2 = ops.router_bwd(x, w, logits.detach(), idx, d_logits + dl_aux, d_scores, True)
+    assert torch.equal(xg.grad, dx2)
+    assert torch.equal(wg.grad, dw2)
+
+
+def block_step(w, inp, accumulate=False, grads=None, logit_bias=None):
+    x = inp["x"].to(DEV).requires_grad_()
+    rw = inp["router_weight"].to(DEV).requires_grad_()
+    gu = inp["gate_up_proj"].to(DEV).requires_grad_()
+    dn = inp["down_proj"].to(DEV).requires_grad_()
+    if grads is not None:
+        for p, g in zip((rw, gu, dn), grads):
+            p.grad = g.clone()
+    bias = None if logit_bias is None else logit_bias.to(DEV)
+    out, logits, scores, idx, aux = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob, None, bias, accumulate)
+    torch.autograd.backward([out, aux], [inp["d_out"].to(DEV), torch.tensor(w.aux_coef, device=DEV)])
+    return dict(logits=logits.detach(), scores=scores.detach(), indices=idx, out=out.detach(), aux=aux.detach(),
+                dx=x.grad, d_router=rw.grad, d_gate_up=gu.grad, d_down=dn.grad)
+
+
+@pytest.mark.parametrize("base,tokens", [("c1", 512), ("c2", 512), ("c4", 1024)])
+def test_moe_block_matches_the_separate_ops_and_the_oracle(base, tokens):
+    w = scaled(WORKLOADS[base], tokens)
+    inp = make_block_inputs(w, seed=11, dtype=BF)
+    bias = inp.get("logit_bias")
+    blk = block_step(w, inp, logit_bias=bias)
+    sep = gpu_block_step(w, inp, logit_bias=bias)
+    compare(blk, oracle_step(w, inp, logit_bias=bias), f"{base} block")
+    # Same kernels: the forward and the weight gradients are the same bits.
+    for key in ("logits", "scores", "indices", "out", "aux", "d_router", "d_gate_up", "d_down"):
+        assert torch.equal(blk[key], sep[key]), key
+    # dX: the router's share joins the experts' in fp32 inside the permute
+    # backward, one rounding where autograd rounds the experts' sum first.
+    close_bf16(blk["dx"], sep["dx"], f"{base} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
+
+
+def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
+    w = scaled(WORKLOADS["c2"], 512)
+    inp = make_block_inputs(w, seed=12, dtype=BF)
+    g = gen(13)
+    init = [torch.randn(inp[n].shape, generator=g).mul(1e-3).to(BF).to(DEV)
+            for n in ("router_weight", "gate_up_proj", "down_proj")]
+    fresh = block_step(w, inp)
+    acc = block_step(w, inp, accumulate=True, grads=init)
+    for key, g0 in zip(("d_router", "d_gate_up", "d_down"), init):
+        assert torch.equal(acc[key], g0 + fresh[key]), key  # torch's bf16 add of the fresh gradient
+    assert torch.equal(acc["dx"], fresh["dx"])

@@ -50,7 +50,11 @@ def test_library_size_queries_and_argument_checks_run_without_a_gpu():
     assert lib.moe_aux_loss_workspace_bytes(40, 8) == (3 + 16) * 17 * 4
     assert lib.moe_aux_loss_workspace_bytes(4096, 512) == (1024 + 16) * 1025 * 4
     assert lib.moe_aux_loss_workspace_bytes(1 << 20, 128) == (1024 + 16) * 257 * 4
-    assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) >= 4096 * 128 * 4
+    # one pass for E <= 256 in 16-expert tiles (no split-K partials), split-K otherwise
+    assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) == 0
+    assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 120) >= 4096 * 120 * 4
+    assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 512) >= 4096 * 512 * 4
+    assert lib.moe_router_aux_fwd_workspace_bytes(4096, 2048, 128) == (256 + 16) * 257 * 4
     # invalid sizes are rejected before any HIP call
     rc = lib.moe_grouped_gemm_fwd(None, None, None, 1, 8, 8, 8, None, None)
     assert rc == _lib.MOE_ERR_INVALID
