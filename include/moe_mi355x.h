@@ -60,16 +60,24 @@ int moe_router_logits_fwd(const void* x, const void* wr, float* logits,
                           int64_t T, int64_t H, int64_t E, void* stream);
 
 /* Fused router forward: logits = x · wrᵀ (+ logit_bias[E] when not NULL, f32),
- * then the top-k softmax of moe_router_topk_fwd.  The GEMM is split along H
- * into f32 partials held in the workspace, and one kernel reduces them and
- * selects the top-k per token.  Replaces Qwen3MoeTopKRouter.forward
+ * then the top-k softmax of moe_router_topk_fwd.  For E <= 256 (a multiple
+ * of 16) one kernel runs the GEMM, the reduction and the selection (no
+ * workspace: the size query returns 0); otherwise the GEMM is split along H
+ * into f32 partials held in the workspace and a second kernel reduces them
+ * and selects.  With logits_bf16 (bf16 [T,E], may be NULL) the logits are
+ * those of a bf16 linear, as the reference computes them under bf16 autocast
+ * (parallel/parallel/engine/engine.py:141): rounded to bf16 before the
+ * softmax, written there as bf16 and to `logits` as the same values in f32,
+ * and the scores are rounded to bf16 (the reference's cast to the logits'
+ * dtype, modeling_qwen3_moe.py:266).  Replaces Qwen3MoeTopKRouter.forward
  * (TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267); the reference router
  * has no bias (the imbalanced benchmark configuration adds one). */
 size_t moe_router_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
 int moe_router_fwd(const void* x, const void* wr, const float* logit_bias,
-                   float* logits, float* scores, int64_t* indices, int64_t T,
-                   int64_t H, int64_t E, int64_t k, int norm_topk_prob,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   float* logits, void* logits_bf16, float* scores,
+                   int64_t* indices, int64_t T, int64_t H, int64_t E, int64_t k,
+                   int norm_topk_prob, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /* Per token: p = softmax(logits) in fp32; indices = the k largest, sorted
  * descending (ties: lower expert index first); scores = p[indices],
@@ -178,9 +186,10 @@ int moe_rmsnorm_bwd(const void* dx, const void* dx2, const void* h,
  * :514-593).  T >= 1. */
 size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E);
 int moe_router_aux_fwd(const void* x, const void* wr, const float* logit_bias,
-                       const float* token_weight, float* logits, float* scores,
-                       int64_t* indices, int64_t T, int64_t H, int64_t E,
-                       int64_t k, int norm_topk_prob, float* aux, float* stats,
+                       const float* token_weight, float* logits,
+                       void* logits_bf16, float* scores, int64_t* indices,
+                       int64_t T, int64_t H, int64_t E, int64_t k,
+                       int norm_topk_prob, float* aux, float* stats,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ----------------------------------------------------------------- permute */

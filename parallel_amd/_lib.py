@@ -37,7 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_abi_version": (_I, []),
     "moe_router_logits_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "moe_router_fwd_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
-    "moe_router_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "moe_router_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "moe_router_logits_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "moe_router_logits_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _P, _SZ, _P]),
     "moe_router_topk_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
@@ -64,7 +64,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "moe_router_aux_fwd_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
-    "moe_router_aux_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _SZ, _P]),
+    "moe_router_aux_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _SZ, _P]),
 }
 
 _lock = threading.Lock()

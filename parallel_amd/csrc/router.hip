@@ -140,7 +140,7 @@ __device__ __forceinline__ void select_topk(const float (&v)[NPL], int E, int k,
 template <int LPT, int KM>
 __device__ __forceinline__ void write_topk(const SoftmaxStats& st, const int (&sel)[KM], const float (&sl)[KM], int k,
                                            int norm, float* __restrict__ scores, int64_t* __restrict__ indices,
-                                           int64_t t) {
+                                           int64_t t, bool bf16_scores = false) {
   const int sub = Tok<LPT>::sub();
   int my_idx = 0;
   float my_logit = -INFINITY;
@@ -155,7 +155,8 @@ __device__ __forceinline__ void write_topk(const SoftmaxStats& st, const int (&s
   const float pv = mine ? expf(my_logit - st.max) / st.sum : 0.0f;
   const float tot = tok_sum<LPT>(pv);
   if (mine) {
-    scores[t * k + sub] = norm ? pv / tot : pv;
+    const float sc = norm ? pv / tot : pv;
+    scores[t * k + sub] = bf16_scores ? bf16_to_f32(f32_to_bf16(sc)) : sc;
     indices[t * k + sub] = my_idx;
   }
 }
@@ -207,12 +208,17 @@ __device__ __forceinline__ void aux_block_partial(float (*part)[2 * LPT * NPL + 
 // entries past E are ignored): adds the bias, writes the logits, the top-k
 // softmax scores and indices and, with_aux, the token's aux terms (the
 // arithmetic of aux_partial_kernel's per-slot sums, which start from zero).
+// With logits_b, the logits are those of a bf16 linear (the reference under
+// bf16 autocast, parallel/parallel/engine/engine.py:141): rounded to bf16
+// (after the bias) before the fp32 softmax and top-k, written to logits_b as
+// bf16 and to logits as the same values in fp32; the scores are rounded to
+// bf16 as the reference's cast to the logits' dtype (modeling_qwen3_moe.py:266).
 template <int LPT, int NPL, int KT>
 __device__ __forceinline__ void route_token(float (&v)[NPL], int64_t t, int E, int k, int norm,
                                             const float* __restrict__ bias, float* __restrict__ logits,
-                                            float* __restrict__ scores, int64_t* __restrict__ indices,
-                                            const float* __restrict__ token_weight, bool with_aux, float (&P)[NPL],
-                                            float (&C)[NPL], float& W) {
+                                            bf16_t* __restrict__ logits_b, float* __restrict__ scores,
+                                            int64_t* __restrict__ indices, const float* __restrict__ token_weight,
+                                            bool with_aux, float (&P)[NPL], float (&C)[NPL], float& W) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int sub = Tok<LPT>::sub();
 #pragma unroll
@@ -220,6 +226,11 @@ __device__ __forceinline__ void route_token(float (&v)[NPL], int64_t t, int E, i
     const int e = sub + j * LPT;
     if (e < E) {
       if (bias) v[j] += bias[e];
+      if (logits_b) {
+        const bf16_t b = f32_to_bf16(v[j]);
+        v[j] = bf16_to_f32(b);
+        logits_b[t * E + e] = b;
+      }
       logits[t * E + e] = v[j];
     } else {
       v[j] = -INFINITY;
@@ -229,7 +240,7 @@ __device__ __forceinline__ void route_token(float (&v)[NPL], int64_t t, int E, i
   int sel[KM];
   float sl[KM];
   select_topk<LPT>(v, E, k, sel, sl);
-  write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t);
+  write_topk<LPT>(st, sel, sl, k, norm, scores, indices, t, logits_b != nullptr);
   if (with_aux) {
     const float w = token_weight ? token_weight[t] : 1.0f;
     W = 0.0f + w;
@@ -255,8 +266,8 @@ __device__ __forceinline__ void route_token(float (&v)[NPL], int64_t t, int E, i
 template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kernel(
     const float* __restrict__ partials, int splits, const float* __restrict__ bias, float* __restrict__ logits,
-    float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k_rt, int norm,
-    const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
+    bf16_t* __restrict__ logits_b, float* __restrict__ scores, int64_t* __restrict__ indices, int T, int E, int k_rt,
+    int norm, const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
   const int k = KT ? KT : k_rt;
   __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];  // E <= LPT NPL
   const int sub = Tok<LPT>::sub();
@@ -295,8 +306,8 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
         v[j] += e < E ? partials[sp * plane + static_cast<int64_t>(t) * E + e] : 0.0f;
       }
     }
-    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, scores, indices, token_weight, aux_ws != nullptr, P,
-                              C, W);
+    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, logits_b, scores, indices, token_weight,
+                              aux_ws != nullptr, P, C, W);
   }  // t < T
   if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
@@ -316,8 +327,9 @@ constexpr int kFusedTokens = 16;
 template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
-    float* __restrict__ logits, float* __restrict__ scores, int64_t* __restrict__ indices, int T, int H, int E,
-    int k_rt, int norm, const float* __restrict__ token_weight, float* __restrict__ aux_ws) {
+    float* __restrict__ logits, bf16_t* __restrict__ logits_b, float* __restrict__ scores,
+    int64_t* __restrict__ indices, int T, int H, int E, int k_rt, int norm, const float* __restrict__ token_weight,
+    float* __restrict__ aux_ws) {
   constexpr int LPT = 16;
   constexpr int NE = NPL;          // 16-expert tiles covered (E <= 16 NPL)
   constexpr int ROW = 16 * NE + 4;  // padded LDS row: the four 4-token row groups of a tile hit distinct banks
@@ -413,8 +425,8 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
       const int e = sub + j * LPT;
       v[j] = ((wpart[0][slot][e] + wpart[1][slot][e]) + wpart[2][slot][e]) + wpart[3][slot][e];
     }
-    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, scores, indices, token_weight, aux_ws != nullptr, P,
-                              C, W);
+    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, logits_b, scores, indices, token_weight,
+                              aux_ws != nullptr, P, C, W);
   }
   if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
@@ -921,15 +933,16 @@ bool router_fused(int64_t T, int64_t H, int64_t E) {
 // logits, scores and indices of T >= 1 tokens and, with aux_ws, the aux
 // partials of token_blocks(T, E) blocks; `partials` is the split-K workspace
 // of the two-pass path (other expert counts).
-int route_tokens(const void* x, const void* wr, const float* bias, float* logits, float* scores, int64_t* indices,
-                 int64_t T, int64_t H, int64_t E, int64_t k, int norm, const float* token_weight, float* aux_ws,
-                 float* partials, hipStream_t st, const char* name) {
+int route_tokens(const void* x, const void* wr, const float* bias, float* logits, void* logits_bf16, float* scores,
+                 int64_t* indices, int64_t T, int64_t H, int64_t E, int64_t k, int norm, const float* token_weight,
+                 float* aux_ws, float* partials, hipStream_t st, const char* name) {
+  bf16_t* logits_b = static_cast<bf16_t*>(logits_bf16);
   const int blocks = token_blocks(T, E);
   if (router_fused(T, H, E)) {
     with_npl_k(E, k, [&](auto, auto N, auto K) {
       hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
                          dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
-                         static_cast<const bf16_t*>(wr), bias, logits, scores, indices, static_cast<int>(T),
+                         static_cast<const bf16_t*>(wr), bias, logits, logits_b, scores, indices, static_cast<int>(T),
                          static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm, token_weight, aux_ws);
     });
     return launch_status(name);
@@ -941,8 +954,8 @@ int route_tokens(const void* x, const void* wr, const float* bias, float* logits
   if (rc) return rc;
   with_npl_k(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_reduce_topk_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
-                       dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits, bias, logits, scores,
-                       indices, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm, token_weight,
+                       dim3(blocks), dim3(kRouterWaves * kWave), 0, st, partials, splits, bias, logits, logits_b,
+                       scores, indices, static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm, token_weight,
                        aux_ws);
   });
   return launch_status(name);
@@ -956,9 +969,9 @@ extern "C" size_t moe_router_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E
   return static_cast<size_t>(splits) * static_cast<size_t>(T) * static_cast<size_t>(E) * sizeof(float);
 }
 
-extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_bias, float* logits, float* scores,
-                              int64_t* indices, int64_t T, int64_t H, int64_t E, int64_t k, int norm_topk_prob,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_bias, float* logits,
+                              void* logits_bf16, float* scores, int64_t* indices, int64_t T, int64_t H, int64_t E,
+                              int64_t k, int norm_topk_prob, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
   MOE_REQUIRE(wr && (T == 0 || (x && logits && scores && indices)), MOE_ERR_INVALID, "router fwd: null pointer");
@@ -969,8 +982,8 @@ extern "C" int moe_router_fwd(const void* x, const void* wr, const float* logit_
   const size_t need = moe_router_fwd_workspace_bytes(T, H, E);
   MOE_REQUIRE((workspace || need == 0) && workspace_bytes >= need, MOE_ERR_WORKSPACE,
               "router fwd: workspace %zu < %zu bytes", workspace_bytes, need);
-  return route_tokens(x, wr, logit_bias, logits, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0, nullptr,
-                      nullptr, static_cast<float*>(workspace), as_stream(stream), "moe_router_fwd");
+  return route_tokens(x, wr, logit_bias, logits, logits_bf16, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0,
+                      nullptr, nullptr, static_cast<float*>(workspace), as_stream(stream), "moe_router_fwd");
 }
 
 extern "C" size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
@@ -981,9 +994,9 @@ extern "C" size_t moe_router_aux_fwd_workspace_bytes(int64_t T, int64_t H, int64
 }
 
 extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* logit_bias, const float* token_weight,
-                                  float* logits, float* scores, int64_t* indices, int64_t T, int64_t H, int64_t E,
-                                  int64_t k, int norm_topk_prob, float* aux, float* stats, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+                                  float* logits, void* logits_bf16, float* scores, int64_t* indices, int64_t T,
+                                  int64_t H, int64_t E, int64_t k, int norm_topk_prob, float* aux, float* stats,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
   MOE_REQUIRE(x && wr && logits && scores && indices && aux && stats, MOE_ERR_INVALID,
@@ -998,8 +1011,8 @@ extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* lo
   float* partials = static_cast<float*>(workspace);
   float* aux_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + moe_router_fwd_workspace_bytes(T, H, E));
   hipStream_t st = as_stream(stream);
-  rc = route_tokens(x, wr, logit_bias, logits, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0, token_weight,
-                    aux_ws, partials, st, "moe_router_aux_fwd(route)");
+  rc = route_tokens(x, wr, logit_bias, logits, logits_bf16, scores, indices, T, H, E, k, norm_topk_prob ? 1 : 0,
+                    token_weight, aux_ws, partials, st, "moe_router_aux_fwd(route)");
   if (rc) return rc;
   return aux_reduce_finalize(aux_ws, token_blocks(T, E), E, stats, aux, st, "moe_router_aux_fwd(reduce)");
 }

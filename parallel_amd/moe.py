@@ -42,7 +42,10 @@ class MoeConfig:
 
 
 class TopKRouter(nn.Module):
-    """Qwen3MoeTopKRouter: fp32 logits, softmax top-k, optional renormalisation."""
+    """Qwen3MoeTopKRouter: softmax top-k over the router logits, optional
+    renormalisation.  The logits are fp32, or, under CUDA bf16 autocast (the
+    reference's default AMP, parallel/parallel/engine/engine.py:141), those
+    of a bf16 linear with bf16 scores, as the reference module gives there."""
 
     def __init__(self, config):
         super().__init__()
@@ -54,6 +57,10 @@ class TopKRouter(nn.Module):
 
     def forward(self, hidden_states: Tensor) -> tuple[Tensor, Tensor, Tensor]:
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            with torch.autocast("cuda", enabled=False):
+                return ops.router_fwd_bf16(hidden_states.to(torch.bfloat16), self.weight.to(torch.bfloat16),
+                                           self.top_k, self.norm_topk_prob)[:3]
         return ops.router_fwd(hidden_states, self.weight, self.top_k, self.norm_topk_prob)
 
 

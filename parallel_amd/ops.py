@@ -6,6 +6,7 @@ the host.  There is no CPU implementation: CPU tensors raise ``ValueError``.
 
 Ops (namespace ``parallel_amd``):
   router_fwd / router_bwd          router GEMM + top-k softmax (+ backward)
+  router_fwd_bf16                  the same with the logits of a bf16 linear (the reference's AMP)
   router_topk                      top-k softmax of given fp32 logits
   aux_loss_fwd / aux_loss_bwd      Switch load-balancing loss
   permute_fwd                      stable sort of routed slots + row gather
@@ -103,7 +104,7 @@ def router_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool,
     idx = torch.empty(T, top_k, dtype=torch.int64, device=x.device)
     bias = None if logit_bias is None else logit_bias.to(device=x.device, dtype=torch.float32).contiguous()
     ws = _ws(_lib.load().moe_router_fwd_workspace_bytes(T, H, E), x.device)
-    call("moe_router_fwd", ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(scores), ptr(idx), T, H, E, top_k,
+    call("moe_router_fwd", ptr(x), ptr(weight), ptr(bias), ptr(logits), None, ptr(scores), ptr(idx), T, H, E, top_k,
          int(norm_topk_prob), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
     return logits, scores, idx
 
@@ -183,6 +184,61 @@ def _router_backward(ctx, d_logits, d_scores, _d_idx):
 
 
 router_fwd.register_autograd(_router_backward, setup_context=_router_setup)
+
+
+@torch.library.custom_op(f"{LIB}::router_fwd_bf16", mutates_args=())
+def router_fwd_bf16(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool,
+                    logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """router_fwd with the logits of a bf16 linear, as Qwen3MoeTopKRouter computes
+    them under the reference's bf16 autocast (parallel/parallel/engine/engine.py:141,
+    TF modeling_qwen3_moe.py:258-267): (logits [T,E] bf16, scores [T,k] bf16,
+    indices, and the same logits in fp32 for the backward).  The softmax and
+    top-k run in fp32 on the bf16 logits; the scores are rounded to bf16."""
+    _require_gpu(x, weight)
+    _require_bf16("router input", x)
+    _require_bf16("router weight", weight)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    T, H = x.shape
+    E = weight.shape[0]
+    dev = x.device
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    logits_b = torch.empty(T, E, dtype=BF16, device=dev)
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    bias = None if logit_bias is None else logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    ws = _ws(_lib.load().moe_router_fwd_workspace_bytes(T, H, E), dev)
+    call("moe_router_fwd", ptr(x), ptr(weight), ptr(bias), ptr(logits), ptr(logits_b), ptr(scores), ptr(idx), T, H,
+         E, top_k, int(norm_topk_prob), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
+    # scores hold bf16 values; the cast is exact
+    return logits_b, scores.to(BF16), idx, logits
+
+
+@router_fwd_bf16.register_fake
+def _(x, weight, top_k, norm_topk_prob, logit_bias=None):
+    T, E = x.shape[0], weight.shape[0]
+    return (x.new_empty(T, E, dtype=BF16), x.new_empty(T, top_k, dtype=BF16),
+            x.new_empty(T, top_k, dtype=torch.int64), x.new_empty(T, E, dtype=torch.float32))
+
+
+def _router_bf16_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
+    x, weight, top_k, norm, _bias = inputs
+    _, _, idx, logits = output
+    ctx.save_for_backward(x, weight, logits, idx)
+    ctx.norm = norm
+    ctx.mark_non_differentiable(idx, logits)
+
+
+def _router_bf16_backward(ctx, d_logits, d_scores, _d_idx, _d_logits32):
+    x, weight, logits, idx = ctx.saved_tensors
+    dl = None if d_logits is None else d_logits.float()
+    ds = None if d_scores is None else d_scores.float()
+    dx, dw = router_bwd_kernels(x, weight, logits, idx, dl, ds, ctx.norm)
+    return dx, dw, None, None, None
+
+
+router_fwd_bf16.register_autograd(_router_bf16_backward, setup_context=_router_bf16_setup)
 
 
 # ----------------------------------------------------------------- aux loss
@@ -333,8 +389,8 @@ def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bi
     bias = None if logit_bias is None else logit_bias.to(device=dev, dtype=torch.float32).contiguous()
     tw = None if token_weight is None else token_weight.float().contiguous()
     ws = _ws(_lib.load().moe_router_aux_fwd_workspace_bytes(T, H, E), dev)
-    call("moe_router_aux_fwd", ptr(x), ptr(weight), ptr(bias), ptr(tw), ptr(logits), ptr(scores), ptr(idx), T, H, E,
-         top_k, int(norm_topk_prob), ptr(aux), ptr(stats), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
+    call("moe_router_aux_fwd", ptr(x), ptr(weight), ptr(bias), ptr(tw), ptr(logits), None, ptr(scores), ptr(idx), T,
+         H, E, top_k, int(norm_topk_prob), ptr(aux), ptr(stats), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
     return logits, scores, idx, aux, stats
 
 

@@ -113,3 +113,74 @@ def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
     for key, g0 in zip(("d_router", "d_gate_up", "d_down"), init):
         assert torch.equal(acc[key], g0 + fresh[key]), key  # torch's bf16 add of the fresh gradient
     assert torch.equal(acc["dx"], fresh["dx"])
+
+
+# ------------------------------------------------- bf16 router logits (AMP)
+
+
+@pytest.mark.parametrize("T,H,E,k,norm", [(1000, 256, 64, 6, True), (4096, 2048, 128, 8, True),
+                                          (300, 72, 120, 8, False), (257, 136, 32, 3, True)])
+def test_bf16_logit_router_routes_bit_exactly(T, H, E, k, norm):
+    """Under the reference's bf16 autocast (parallel/parallel/engine/engine.py:141)
+    Qwen3MoeTopKRouter's F.linear gives bf16 logits; softmax and top-k run in
+    fp32 on them and the scores are cast back to bf16 (TF
+    modeling_qwen3_moe.py:258-267)."""
+    x = torch.randn(T, H, generator=gen(T + 1)).to(BF)
+    w = (torch.randn(E, H, generator=gen(E + 1)) * 0.05).to(BF)
+    logits_b, scores, idx, logits32 = ops.router_fwd_bf16(x.to(DEV), w.to(DEV), k, norm)
+    assert logits_b.dtype == BF and scores.dtype == BF and logits32.dtype == torch.float32
+    lb = logits_b.cpu()
+    assert torch.equal(logits32.cpu(), lb.float())
+    # The bf16 logits round the fp32 sum: mostly the same bits as rounding the
+    # oracle's fp32 sum, and always within one bf16 step of it plus the fp32
+    # accumulation-order noise (which exceeds a bf16 step only near zero).
+    ref = O.router_logits(x, w)
+    want = ref.to(BF)
+    step = torch.ldexp(torch.ones_like(ref), torch.frexp(ref)[1] - 8)  # one bf16 ulp at each value
+    assert ((lb.float() - ref).abs() <= step + 1e-5).all()
+    assert (lb == want).float().mean() > 0.99
+    # Routing on these logits is exact, ties included: largest logit first,
+    # equal logits in increasing expert index, the reference's fp32 softmax,
+    # renormalisation and bf16 cast.
+    canon = torch.argsort(-lb.float(), dim=-1, stable=True)[:, :k]
+    assert torch.equal(idx.cpu(), canon)
+    top = torch.softmax(lb.float(), dim=-1).gather(1, canon)
+    if norm:
+        top = top / top.sum(dim=-1, keepdim=True)
+    assert torch.equal(scores.cpu(), top.to(BF))
+    # torch.topk (the oracle) agrees wherever its tie order does not matter
+    ref_s, ref_i = O.topk_softmax(lb, k, norm)
+    ties = O.topk_ties(lb.float(), ref_i)
+    routing_check(idx, ref_i, lb.float(), expect_ties=int(ties.sum()))
+
+
+def test_bf16_logit_router_backward_and_the_autocast_module():
+    from parallel_amd import TopKRouter
+
+    T, H, E, k = 512, 256, 64, 6
+    x = torch.randn(T, H, generator=gen(31)).to(BF)
+    w = (torch.randn(E, H, generator=gen(32)) * 0.05).to(BF)
+    d_scores = torch.randn(T, k, generator=gen(33))
+    xg, wg = x.to(DEV).requires_grad_(), w.to(DEV).requires_grad_()
+    logits_b, scores, idx, _ = ops.router_fwd_bf16(xg, wg, k, True)
+    scores.backward(d_scores.to(DEV).to(BF))
+    # fp32 autograd of the reference's softmax / gather / renormalisation on
+    # the selection made (bf16 logits tie often; the selection itself is pinned
+    # bit for bit above), the bf16 rounding of the logits passed straight through
+    xr, wr = x.float().requires_grad_(), w.float().requires_grad_()
+    lr = O.router_logits(xr, wr)
+    lr = lr + (lr.to(BF).float() - lr).detach()
+    sr = torch.softmax(lr, dim=-1).gather(1, idx.cpu())
+    sr = sr / sr.sum(dim=-1, keepdim=True)
+    sr.backward(d_scores.to(BF).float())
+    close_bf16(xg.grad, xr.grad, "bf16-logit router dx")
+    close_bf16(wg.grad, wr.grad, "bf16-logit router dweight")
+    # The transformers-facing module takes this path under bf16 autocast.
+    cfg = type("Cfg", (), dict(num_experts_per_tok=k, num_experts=E, norm_topk_prob=True, hidden_size=H))()
+    router = TopKRouter(cfg).to(DEV)
+    with torch.no_grad():
+        router.weight.copy_(w.float())
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        lm, sm, im = router(x.to(DEV))
+    assert lm.dtype == BF and sm.dtype == BF
+    assert torch.equal(lm, logits_b.detach()) and torch.equal(im, idx) and torch.equal(sm, scores.detach())

@@ -178,7 +178,7 @@ def test_zero_size_calls_accept_null_buffers_without_a_gpu():
         "fwd": lambda: lib.moe_grouped_gemm_fwd(None, b, b, E, 0, H, I, None, None),
         "dgrad": lambda: lib.moe_grouped_gemm_dgrad(None, b, b, E, 0, 2 * I, H, None, None),
         "dgrad_swiglu": lambda: lib.moe_grouped_gemm_dgrad_swiglu_bwd(None, b, None, b, E, 0, H, I, None, None),
-        "router_fwd": lambda: lib.moe_router_fwd(None, b, None, None, None, None, 0, H, E, k, 1, b, 16, None),
+        "router_fwd": lambda: lib.moe_router_fwd(None, b, None, None, None, None, None, 0, H, E, k, 1, b, 16, None),
         "topk_fwd": lambda: lib.moe_router_topk_fwd(None, None, None, 0, E, k, 1, None),
         "topk_bwd": lambda: lib.moe_router_topk_bwd(None, None, None, 0, E, k, 1, None, 0, None, None),
         "topk_bwd_bf16": lambda: lib.moe_router_topk_bwd_bf16(None, None, None, None, 0, E, k, 1, None, None),
