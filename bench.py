@@ -57,12 +57,14 @@ def kernel_work(w, T: int, S: int):
         "up_wgrad": (4.0 * S * H * I, pre + xp + Wgu),
         "router_fwd": (2.0 * T * H * E, T * H * b + E * H * b + 8.0 * T * E + 12.0 * T * k),
         "router_gemm_bwd": (4.0 * T * H * E, T * E * b + T * H * b + E * H * b + T * H * b + 4.0 * E * H),
-        # read x rows once per route and the routes, write permuted rows and maps
+        # read each x row once and the routes, write permuted rows and maps
         "permute_fwd": (None, T * H * b + S * H * b + 16.0 * S),
         "combine_fwd": (None, S * H * b + 8.0 * S + T * H * b),
         "combine_bwd": (None, T * H * b + 2.0 * S * H * b + 12.0 * S),
-        "permute_bwd": (None, S * H * b + T * H * b + 4.0 * S),
-        "router_topk_bwd": (None, 8.0 * T * E + 2.0 * T * E + 16.0 * T * k),
+        # the routes' rows, the router's dX added in (d_add), and d_hidden
+        "permute_bwd": (None, S * H * b + 2.0 * T * H * b + 4.0 * S),
+        # logits in, bf16 d_logits out (the aux gradient formed in the same pass)
+        "router_topk_bwd": (None, 4.0 * T * E + 2.0 * T * E + 16.0 * T * k),
         "aux_fwd": (None, 4.0 * T * E),
         "aux_bwd": (None, 8.0 * T * E),
     }
@@ -87,17 +89,18 @@ def read_traffic(tag: str, workload: str):
 
 # Kernels launched by each timed entry point (tag), matched on demangled names.
 _TAG_KERNELS = {
+    "router_fused_fwd_kernel": "router_fwd",
     "router_reduce_topk_kernel": "router_fwd",
     "reduce_partials_bf16_kernel": "router_gemm_bwd",
     "router_topk_bwd_kernel": "router_topk_bwd",
     "aux_partial_kernel": "aux_fwd",
-    "aux_reduce_kernel": "aux_fwd",
-    "aux_finalize_kernel": "aux_fwd",
+    "aux_reduce_kernel": "router_fwd",  # in the step, moe_router_aux_fwd's loss reduction
+    "aux_finalize_kernel": "router_fwd",
     "aux_bwd_kernel": "aux_bwd",
     "permute_count_kernel": "permute_fwd",
     "permute_scan_kernel": "permute_fwd",
     "permute_scatter_kernel": "permute_fwd",
-    "gather_rows_kernel": "permute_fwd",
+    "scatter_rows_kernel": "permute_fwd",
     "combine_fwd_kernel": "combine_fwd",
     "combine_bwd_kernel": "combine_bwd",
     "permute_bwd_kernel": "permute_bwd",
