@@ -15,7 +15,9 @@ microseconds of stream time).  The per-entry-point table comes from an
 untimed instrumented pass (events around every launch) after the warm-up,
 which also picks the dominant kernel.  The CPU
 baseline times the reference's op sequence (F.grouped_mm on the CPU, the
-config's dtype) on a bounded sample of the same layer.
+config's dtype) on a bounded sample of the same layer.  After the C2
+headline the run also times the MFMA-bound layers C4 and C5 briefly
+(`other_configs` in the same JSON line; `--no-other-configs` skips them).
 """
 
 from __future__ import annotations
@@ -362,61 +364,22 @@ def cpu_baseline(w, tokens: int):
     }
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", help="workload key (c2 c3 c4 c5); c2 is the headline")
-    ap.add_argument("--instrumented-steps", type=int, default=3,
-                    help="untimed steps with events around every launch (the per-kernel table)")
-    ap.add_argument("--cpu-baseline-tokens", type=int, default=4096)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a 1 GiB device copy 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
-    ap.add_argument("--profile-summary", action="store_true",
-                    help="write profiles/ summaries from rocprofv3 outputs (--trace-csv, --pmc-*, --cal-*)")
-    ap.add_argument("--trace-csv", help="kernel_trace.csv of a rocprofv3 --kernel-trace --stats run")
-    ap.add_argument("--pmc-fetch")
-    ap.add_argument("--pmc-write")
-    ap.add_argument("--cal-fetch")
-    ap.add_argument("--cal-write")
-    ap.add_argument("--pmc-calls", type=int, default=6,
-                    help="entry-point calls in the --pmc runs: warm-up + instrumented + timed steps (1 + 3 + 2)")
-    ap.add_argument("--steps-profiled", type=int, default=10)
-    ap.add_argument("--profile-commands", help="the rocprofv3 command lines, one per line, recorded in the summaries")
-    ap.add_argument("--pmc-util", help="counter_collection dir of a --pmc MfmaUtil LdsUtil LdsBankConflict run")
-    ap.add_argument("--pmc-ta", help="counter_collection dir of the texture-unit counter run")
-    ap.add_argument("--pmc-tcp", help="counter_collection dir of the L1 (TCP) counter run")
-    args = ap.parse_args()
-    if args.profile_summary:
-        sys.path.insert(0, str(ROOT))
-        return profile_summary(args)
-    if args.copy_calibration:
-        import torch
-
-        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log("copied 1 GiB three times")
-        return 0
-    if args.gpus != 1:
-        print(
-            f"bench.py runs one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-            "it measures one rank's share on one MI355X",
-            file=sys.stderr,
-        )
-        return 2
-
+def measure(w, steps: int, warmup: int, instrumented_steps: int):
+    """Builds workload w's inputs on the GPU, runs `warmup` steps, an
+    instrumented pass (events around every launch, outside the timed region)
+    and `steps` timed steps in which only the dominant entry point carries
+    events.  Returns the step time, the per-entry-point durations and the
+    dominant entry point's launches in the timed region."""
     import torch
 
-    sys.path.insert(0, str(ROOT))
     from parallel_amd import _lib, ops
-    from parallel_amd.workloads import WORKLOADS, make_block_inputs
+    from parallel_amd.workloads import make_block_inputs
 
-    w = WORKLOADS[args.config]
+    class _Args:
+        pass
+
+    args = _Args()
+    args.steps, args.warmup, args.instrumented_steps = steps, warmup, instrumented_steps
     dev = "cuda"
     torch.manual_seed(0)
     inp = make_block_inputs(w, seed=0, device=dev, dtype=torch.bfloat16, weights_on_device_rng=True)
@@ -509,6 +472,72 @@ def main() -> int:
     tokens_per_s = w.sources * w.tokens * args.steps / elapsed  # source tokens (one source but for C3)
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:,.0f} tokens/s")
 
+    return dict(ms_per_step=ms_per_step, tokens_per_s=tokens_per_s, elapsed=elapsed, durations=durations,
+                dominant=dominant, dominant_ms=dominant_ms, rows=rows)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", help="workload key (c2 c3 c4 c5); c2 is the headline")
+    ap.add_argument("--instrumented-steps", type=int, default=3,
+                    help="untimed steps with events around every launch (the per-kernel table)")
+    ap.add_argument("--cpu-baseline-tokens", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the C4/C5 side measurements after the C2 headline")
+    ap.add_argument("--other-steps", type=int, default=10, help="timed steps of each C4/C5 side measurement")
+    ap.add_argument("--profile-summary", action="store_true",
+                    help="write profiles/ summaries from rocprofv3 outputs (--trace-csv, --pmc-*, --cal-*)")
+    ap.add_argument("--trace-csv", help="kernel_trace.csv of a rocprofv3 --kernel-trace --stats run")
+    ap.add_argument("--pmc-fetch")
+    ap.add_argument("--pmc-write")
+    ap.add_argument("--cal-fetch")
+    ap.add_argument("--cal-write")
+    ap.add_argument("--pmc-calls", type=int, default=6,
+                    help="entry-point calls in the --pmc runs: warm-up + instrumented + timed steps (1 + 3 + 2)")
+    ap.add_argument("--steps-profiled", type=int, default=10)
+    ap.add_argument("--profile-commands", help="the rocprofv3 command lines, one per line, recorded in the summaries")
+    ap.add_argument("--pmc-util", help="counter_collection dir of a --pmc MfmaUtil LdsUtil LdsBankConflict run")
+    ap.add_argument("--pmc-ta", help="counter_collection dir of the texture-unit counter run")
+    ap.add_argument("--pmc-tcp", help="counter_collection dir of the L1 (TCP) counter run")
+    args = ap.parse_args()
+    if args.profile_summary:
+        sys.path.insert(0, str(ROOT))
+        return profile_summary(args)
+    if args.copy_calibration:
+        import torch
+
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 1 GiB three times")
+        return 0
+    if args.gpus != 1:
+        print(
+            f"bench.py runs one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+            "it measures one rank's share on one MI355X",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from parallel_amd import _lib, ops
+    from parallel_amd.workloads import WORKLOADS, make_block_inputs
+
+    w = WORKLOADS[args.config]
+    m = measure(w, args.steps, args.warmup, args.instrumented_steps)
+    ms_per_step, tokens_per_s, elapsed = m["ms_per_step"], m["tokens_per_s"], m["elapsed"]
+    durations, dominant, dominant_ms, rows = m["durations"], m["dominant"], m["dominant_ms"], m["rows"]
+
     if w.local_experts:  # the experts see `rows` tokens of one route each, over the local experts
         import dataclasses
 
@@ -552,6 +581,32 @@ def main() -> int:
     gemm_flops = w.gemm_flops(rows)  # fwd + bwd over the routed rows
     gemm_tflops = gemm_flops / gemm_s / 1e12 if gemm_s else None
 
+    # The MFMA-bound layers (C4: imbalanced routing, dW accumulated; C5: the
+    # larger layer) timed briefly after the headline, in the same process.
+    other = {}
+    if args.config == "c2" and not args.no_other_configs:
+        import gc
+
+        del m
+        gc.collect()
+        torch.cuda.empty_cache()
+        for name in ("c4", "c5"):
+            wo = WORKLOADS[name]
+            mo = measure(wo, args.other_steps, 2, 2)
+            tags = [t for t in ("up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "up_dgrad", "up_wgrad")
+                    if t in mo["durations"]]
+            g_s = sum(statistics.fmean(mo["durations"][t]) for t in tags) * 1e-3
+            g_tf = wo.gemm_flops(mo["rows"]) / g_s / 1e12
+            other[name] = {"ms_per_step": round(mo["ms_per_step"], 4), "tokens_per_s": round(mo["tokens_per_s"], 1),
+                           "steps": args.other_steps, "warmup": 2, "tokens": wo.tokens, "hidden": wo.hidden,
+                           "moe_intermediate": wo.intermediate,
+                           "grouped_gemm": {"time_ms": round(g_s * 1e3, 4), "tflops": round(g_tf, 1),
+                                            "mfma_frac": round(g_tf / MFMA_BF16_PEAK_TFLOPS, 4)}}
+            log(f"{name}: {mo['ms_per_step']:.3f} ms/step, grouped GEMMs {g_tf:.0f} TFLOP/s")
+            del mo
+            gc.collect()
+            torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline and not w.local_experts:
         log(f"cpu baseline: {args.cpu_baseline_tokens} tokens on {torch.get_num_threads()} threads")
@@ -583,6 +638,10 @@ def main() -> int:
         "kernels_source": f"untimed instrumented pass of {args.instrumented_steps} steps (events around every launch)",
         "cpu_baseline": cpu,
     }
+    if other:
+        result["other_configs"] = other
+        result["other_configs_note"] = ("C4 and C5 step times in the same run (value is C2's); grouped_gemm from "
+                                         "an instrumented pass of 2 steps")
     if w.local_experts:
         result["config"].update(sources=w.sources, local_experts=w.local_experts, routed_rows=rows,
                                 zipf_alpha=w.zipf_alpha)
