@@ -32,7 +32,12 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (the fp32 path, C1)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def mfma_peak(w) -> float:
+    return MFMA_FP32_PEAK_TFLOPS if w.dtype == "fp32" else MFMA_BF16_PEAK_TFLOPS
 
 
 def log(*a):
@@ -43,11 +48,11 @@ def kernel_work(w, T: int, S: int):
     """Algorithmic work per launch, per timer tag: (flops or None, bytes).
 
     Bytes are the HBM traffic of an ideal kernel: every operand read once and
-    every output written once (bf16 activations and weights, fp32 router
-    logits and scores).  A kernel's bound is whichever of flops / MFMA peak and
-    bytes / HBM peak is larger."""
+    every output written once (bf16 activations and weights, or fp32 for
+    the fp32 path; fp32 router logits and scores).  A kernel's bound is
+    whichever of flops / MFMA peak and bytes / HBM peak is larger."""
     H, I, E, k = w.hidden, w.intermediate, w.experts, w.top_k
-    b = 2  # bf16
+    b = 4 if w.dtype == "fp32" else 2  # bytes per activation / weight element
     Wgu, Wdn = E * 2 * I * H * b, E * H * I * b  # expert weights
     xp, act, pre, y = S * H * b, S * I * b, S * 2 * I * b, S * H * b  # permuted rows, SwiGLU act, gate|up, down out
     return {
@@ -72,8 +77,8 @@ def kernel_work(w, T: int, S: int):
     }
 
 
-def bound_of(flops, nbytes):
-    if flops is not None and flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9):
+def bound_of(flops, nbytes, peak_tflops=MFMA_BF16_PEAK_TFLOPS):
+    if flops is not None and flops / (peak_tflops * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9):
         return "mfma"
     return "hbm"
 
@@ -246,7 +251,7 @@ def profile_summary(args) -> int:
             f"hbm_bytes_per_launch: {rd + wr:.0f}",
             f"algorithmic_bytes_per_launch: {amount:.0f}",
             f"algorithmic_flops_per_launch: {flops:.0f}" if flops is not None else "algorithmic_flops_per_launch: -",
-            f"bound: {bound_of(flops, amount)}",
+            f"bound: {bound_of(flops, amount, mfma_peak(w))}",
         ]
         (prof / f"{tag}_{w.name}_pmc.txt").write_text("\n".join(body) + "\n")
     log(f"wrote {len(by_tag)} traffic summaries and kernel_stats_{w.name}.txt under {prof}")
@@ -341,13 +346,14 @@ def cpu_baseline(w, tokens: int):
     from parallel_amd.workloads import make_block_inputs, scaled
 
     ws = scaled(w, tokens)
-    inp = make_block_inputs(ws, seed=0, dtype=torch.bfloat16)
+    dtype = torch.float32 if w.dtype == "fp32" else torch.bfloat16
+    inp = make_block_inputs(ws, seed=0, dtype=dtype)
     leaves = O.make_leaves(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"])
     times = []
     for i in range(4):
         t0 = time.perf_counter()
         O.reference_step(leaves, inp["d_out"], top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=w.aux_coef,
-                         compute_dtype=torch.bfloat16, logit_bias=inp.get("logit_bias"))
+                         compute_dtype=dtype, logit_bias=inp.get("logit_bias"))
         times.append(time.perf_counter() - t0)
     med = statistics.median(times[1:])
     return {
@@ -359,7 +365,7 @@ def cpu_baseline(w, tokens: int):
         "torch_threads": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{tokens} tokens of the {w.name} layer (H={w.hidden}, E={w.experts}, top-{w.top_k}, "
-                  f"I={w.intermediate}), bf16, fwd+bwd via F.grouped_mm on the CPU; median of 3 after 1 warm-up "
+                  f"I={w.intermediate}), {w.dtype}, fwd+bwd via F.grouped_mm on the CPU; median of 3 after 1 warm-up "
                   f"({med:.2f} s/step)",
     }
 
@@ -382,7 +388,8 @@ def measure(w, steps: int, warmup: int, instrumented_steps: int):
     args.steps, args.warmup, args.instrumented_steps = steps, warmup, instrumented_steps
     dev = "cuda"
     torch.manual_seed(0)
-    inp = make_block_inputs(w, seed=0, device=dev, dtype=torch.bfloat16, weights_on_device_rng=True)
+    dtype = torch.float32 if w.dtype == "fp32" else torch.bfloat16  # C1 runs the fp32 path
+    inp = make_block_inputs(w, seed=0, device=dev, dtype=dtype, weights_on_device_rng=True)
     gu = inp["gate_up_proj"].requires_grad_()
     dn = inp["down_proj"].requires_grad_()
     if w.local_experts:
@@ -481,7 +488,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", help="workload key (c2 c3 c4 c5); c2 is the headline")
+    ap.add_argument("--config", default="c2",
+                    help="workload key (c1 c2 c3 c4 c5); c2 is the headline, c1 the reference's fp32 CPU case")
     ap.add_argument("--instrumented-steps", type=int, default=3,
                     help="untimed steps with events around every launch (the per-kernel table)")
     ap.add_argument("--cpu-baseline-tokens", type=int, default=4096)
@@ -544,26 +552,27 @@ def main() -> int:
         work = kernel_work(dataclasses.replace(w, experts=w.local_experts, top_k=1), rows, rows)
     else:
         work = kernel_work(w, w.tokens, w.slots)
+    peak = mfma_peak(w)
     kernels = {}
     for tag, ds in sorted(durations.items()):
         avg = statistics.fmean(ds)
         entry = {"avg_ms": round(avg, 4), "launches_per_step": len(ds) // args.instrumented_steps}
         if tag in work:
             flops, nbytes = work[tag]
-            entry["bound"] = bound_of(flops, nbytes)
+            entry["bound"] = bound_of(flops, nbytes, peak)
             if flops is not None:
                 tf = flops / (avg * 1e-3) / 1e12
-                entry.update(tflops=round(tf, 1), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
+                entry.update(tflops=round(tf, 1), mfma_frac=round(tf / peak, 4))
             gbs = nbytes / (avg * 1e-3) / 1e9
             entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
         kernels[tag] = entry
         log(f"  {tag:16s} {avg * 1e3:9.1f} us  {entry}")
     flops, nbytes = work[dominant]
     avg_s = statistics.fmean(dominant_ms) * 1e-3  # measured inside the timed region
-    if bound_of(flops, nbytes) == "mfma":
+    if bound_of(flops, nbytes, peak) == "mfma":
         achieved = flops / avg_s / 1e12
-        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)}
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
     else:
         achieved = nbytes / avg_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -624,15 +633,16 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": w.dtype,
         "data": "synthetic (seeded normal inputs and weights)",
-        "config": {"workload": f"{w.name}: Qwen3-30B-A3B MoE block" if w.name in ("c2", "c4") else w.name,
+        "config": {"workload": {"c1": "c1: tiny Qwen3-MoE block (fp32)", "c2": "c2: Qwen3-30B-A3B MoE block",
+                                "c4": "c4: Qwen3-30B-A3B MoE block"}.get(w.name, w.name),
                    "tokens": w.tokens, "hidden": w.hidden, "experts": w.experts, "top_k": w.top_k,
                    "moe_intermediate": w.intermediate, "router_logits": "fp32", "aux_coef": w.aux_coef,
                    "dW": "accumulated into existing gradients" if w.name == "c4" else "written"},
         "grouped_gemm": {"flops_fwd_bwd": gemm_flops, "time_ms": round(gemm_s * 1e3, 4),
                          "tflops": round(gemm_tflops, 1) if gemm_tflops else None,
-                         "mfma_frac": round(gemm_tflops / MFMA_BF16_PEAK_TFLOPS, 4) if gemm_tflops else None},
+                         "mfma_frac": round(gemm_tflops / peak, 4) if gemm_tflops else None},
         "roofline": roofline,
         "kernels": kernels,
         "kernels_source": f"untimed instrumented pass of {args.instrumented_steps} steps (events around every launch)",

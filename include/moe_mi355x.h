@@ -335,6 +335,57 @@ int moe_grouped_gemm_wgrad_bucket(const void* dc, const void* a,
                                   int64_t bucket_rows, int64_t bucket_stride,
                                   int dw_is_f32, int accumulate, void* stream);
 
+/* ------------------------------------------------------ the fp32 expert path */
+
+/* The reference's grouped experts accept fp32 modules and then compute in
+ * fp32 (TF/integrations/moe.py:377-478).  These entry points run that path
+ * with fp32 operands and arithmetic; the row permutation is moe_permute_fwd
+ * over each row's bytes (H fp32 = 2H bf16-sized units).  They serve small
+ * fp32 layers (the C1 configuration), not the tuned bf16 step.
+ *
+ * Grouped GEMM: C(i, j) = sum_r A(i, r) B(r, j) (+ C(i, j) with accumulate),
+ * A(i, r) = A[i sAi + r sAr], B(r, j) = B[r sBr + j sBj], C(i, j) =
+ * C[i sCi + j sCj], on v_mfma_f32_32x32x2_f32.
+ *   mode 0 (projections, input gradients): output rows i in [0, M) are
+ *     grouped by the inclusive offsets offs[G] (rows of group g use B + g sBg;
+ *     rows from offs[G-1] on are left untouched), r in [0, K);
+ *   mode 1 (weight gradients): reduction rows r in [0, K) are grouped by offs;
+ *     group g writes C + g sCg over i in [0, M), j in [0, N) (zeros, or
+ *     nothing added, for an empty group).
+ * F.grouped_mm of TF/integrations/moe.py:440-459 and its autograd. */
+int moe_f32_grouped_gemm(const float* A, const float* B, const int32_t* offs,
+                         int64_t G, int mode, int64_t M, int64_t N, int64_t K,
+                         int64_t sAi, int64_t sAr, int64_t sBr, int64_t sBj,
+                         int64_t sBg, float* C, int64_t sCi, int64_t sCj,
+                         int64_t sCg, int accumulate, void* stream);
+
+/* act[S,I] = silu(pre[:, :I]) * pre[:, I:] and its backward (d_pre[S,2I]
+ * from d_act[S,I] and pre), over the rows below offsets[num_buckets-1]
+ * (TF/integrations/moe.py:447-450). */
+int moe_f32_swiglu_fwd(const float* pre, float* act, const int32_t* offsets,
+                       int64_t num_buckets, int64_t S, int64_t I, void* stream);
+int moe_f32_swiglu_bwd(const float* d_act, const float* pre, float* d_pre,
+                       const int32_t* offsets, int64_t num_buckets, int64_t S,
+                       int64_t I, void* stream);
+
+/* moe_combine_fwd / moe_combine_bwd / moe_permute_bwd for fp32 rows (same
+ * slot semantics: slots at or past offsets[num_buckets-1] contribute
+ * nothing, and receive zero gradient rows and zero score gradients).  The
+ * permute backward adds d_add[T,H] (may be NULL) after each token's sum. */
+int moe_f32_combine_fwd(const float* y, const int32_t* pos_of_slot,
+                        const int32_t* offsets, int64_t num_buckets,
+                        const float* scores, int64_t T, int64_t H, int64_t k,
+                        float* out, void* stream);
+int moe_f32_combine_bwd(const float* d_out, const float* y,
+                        const int32_t* pos_of_slot, const int32_t* offsets,
+                        int64_t num_buckets, const float* scores, int64_t T,
+                        int64_t H, int64_t k, float* d_y, float* d_scores,
+                        void* stream);
+int moe_f32_permute_bwd(const float* d_xp, const int32_t* pos_of_slot,
+                        const int32_t* offsets, int64_t num_buckets, int64_t T,
+                        int64_t H, int64_t k, const float* d_add, float* d_x,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

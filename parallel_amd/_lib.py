@@ -50,6 +50,13 @@ SIGNATURES: dict[str, tuple] = {
     "moe_permute_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_permute_fwd": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "moe_permute_fwd_noalloc": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "moe_f32_grouped_gemm": (_I, [_P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
+                                  _I64, _I64, _I, _P]),
+    "moe_f32_swiglu_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "moe_f32_swiglu_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "moe_f32_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
+    "moe_f32_combine_bwd": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "moe_f32_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_dispatch_meta": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P]),
     "moe_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),

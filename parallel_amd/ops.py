@@ -93,6 +93,8 @@ def router_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool,
     the softmax; the reference router has none, the imbalanced benchmark
     harness uses it."""
     _require_gpu(x, weight)
+    if x.dtype == weight.dtype == torch.float32:
+        return _router_fwd_f32(x.contiguous(), weight.contiguous(), top_k, norm_topk_prob, logit_bias)
     _require_bf16("router input", x)
     _require_bf16("router weight", weight)
     x = x.contiguous()
@@ -116,6 +118,64 @@ def _(x, weight, top_k, norm_topk_prob, logit_bias=None):
             x.new_empty(T, top_k, dtype=torch.int64))
 
 
+def _one_group(T: int, device) -> Tensor:
+    """Inclusive offsets [T] of a single group (a fill kernel, no host copy)."""
+    return torch.full((1,), T, dtype=torch.int32, device=device)
+
+
+def _router_fwd_f32(x, weight, top_k, norm_topk_prob, logit_bias):
+    """Qwen3MoeTopKRouter.forward of an fp32 module (TF modeling_qwen3_moe.py:258-267,
+    F.linear in fp32): the logits GEMM on fp32 MFMA, then the top-k softmax."""
+    T, H = x.shape
+    E = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError(f"router weight {tuple(weight.shape)} does not match hidden {H}")
+    s = _stream(x)
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    _f32_gemm(x, weight, _one_group(T, x.device), 1, 0, T, E, H, (H, 1), (1, H), 0, logits, (E, 1), 0, False, s,
+              "router_fwd")
+    if logit_bias is not None:
+        logits.add_(logit_bias.to(device=x.device, dtype=torch.float32))
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=x.device)
+    call("moe_router_topk_fwd", ptr(logits), ptr(scores), ptr(idx), T, E, top_k, int(norm_topk_prob), s,
+         tag="router_fwd")
+    return logits, scores, idx
+
+
+def _router_bwd_f32(x, weight, logits, indices, d_logits, d_scores, norm_topk_prob, token_weight, stats, d_aux,
+                    dw_target):
+    """router_bwd_kernels for fp32 modules: the fp32 logits gradient (top-k
+    backward, plus the aux loss's), then dx = dL·W and dW = dLᵀ·x on fp32 MFMA."""
+    T, H = x.shape
+    E = weight.shape[0]
+    k = indices.shape[1]
+    s = _stream(x)
+    if d_logits is not None:
+        dl = d_logits.float().contiguous().clone()
+        accumulate = 1
+    else:
+        dl = torch.empty(T, E, dtype=torch.float32, device=x.device)
+        accumulate = 0
+    if d_scores is None:
+        d_scores = torch.zeros(T, k, dtype=torch.float32, device=x.device)
+    call("moe_router_topk_bwd", ptr(logits), ptr(indices), ptr(d_scores.float().contiguous()), T, E, k,
+         int(norm_topk_prob), ptr(dl), accumulate, None, s, tag="router_topk_bwd")
+    if d_aux is not None:
+        tw = None if token_weight is None else token_weight.float().contiguous()
+        call("moe_aux_loss_bwd", ptr(logits), ptr(tw), ptr(stats), ptr(d_aux.float().reshape(1).contiguous()), T, E,
+             ptr(dl), 1, s, tag="router_topk_bwd")
+    one = _one_group(T, x.device)
+    dx = torch.empty(T, H, dtype=torch.float32, device=x.device)
+    _f32_gemm(dl, weight, one, 1, 0, T, H, E, (E, 1), (H, 1), 0, dx, (H, 1), 0, False, s, "router_gemm_bwd")
+    fresh = dw_target is None or dw_target.dtype != torch.float32
+    dw = torch.empty(E, H, dtype=torch.float32, device=x.device) if fresh else dw_target
+    _f32_gemm(dl, x, one, 1, 1, E, H, T, (1, E), (H, 1), 0, dw, (H, 1), 0, not fresh, s, "router_gemm_bwd")
+    if dw_target is not None and fresh:
+        dw_target.add_(dw)
+    return dx, (None if dw_target is not None else dw)
+
+
 def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
                        d_scores: Tensor | None, norm_topk_prob: bool, token_weight: Tensor | None = None,
                        stats: Tensor | None = None, d_aux: Tensor | None = None,
@@ -126,7 +186,11 @@ def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tenso
     ``d_aux`` (and the ``stats``/``token_weight`` of router_aux_fwd) the aux
     loss's logits gradient is added in the same top-k backward pass.  With
     ``dw_target`` (the router weight's existing bf16 gradient) the weight
-    gradient is added into it and None is returned in its place."""
+    gradient is added into it and None is returned in its place.  fp32
+    modules get fp32 gradients from the fp32 kernels."""
+    if x.dtype == weight.dtype == torch.float32:
+        return _router_bwd_f32(x.contiguous(), weight.contiguous(), logits, indices, d_logits, d_scores,
+                               norm_topk_prob, token_weight, stats, d_aux, dw_target)
     x = x.contiguous()
     weight = weight.contiguous()
     T, H = x.shape
@@ -374,6 +438,17 @@ def router_aux_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool, 
 
 def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias):
     _require_gpu(x, weight, token_weight)
+    if x.dtype == weight.dtype == torch.float32:
+        # fp32 modules: the fp32 router, then the aux kernels on its logits
+        logits, scores, idx = _router_fwd_f32(x.contiguous(), weight.contiguous(), top_k, norm_topk_prob, logit_bias)
+        T, E = logits.shape
+        tw = None if token_weight is None else token_weight.float().contiguous()
+        aux = torch.empty((), dtype=torch.float32, device=x.device)
+        stats = torch.empty(E + 1, dtype=torch.float32, device=x.device)
+        ws = _ws(_lib.load().moe_aux_loss_workspace_bytes(T, E), x.device)
+        call("moe_aux_loss_fwd", ptr(logits), ptr(tw), T, E, top_k, ptr(aux), ptr(stats), ptr(ws), ws.numel(),
+             _stream(x), tag="router_fwd")
+        return logits, scores, idx, aux, stats
     _require_bf16("router input", x)
     _require_bf16("router weight", weight)
     x = x.contiguous()
@@ -486,8 +561,12 @@ def _check_experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, g
             f"expert weights do not match: gate_up_proj {tuple(gate_up_proj.shape)}, "
             f"down_proj {tuple(down_proj.shape)}, hidden {H}"
         )
-    for name, t in (("hidden states", hidden), ("gate_up_proj", gate_up_proj), ("down_proj", down_proj)):
-        _require_bf16(name, t)
+    if not (hidden.dtype == gate_up_proj.dtype == down_proj.dtype == torch.float32):
+        # fp32 modules take the fp32 path; everything else runs in bf16
+        for name, t in (("hidden states", hidden), ("gate_up_proj", gate_up_proj), ("down_proj", down_proj)):
+            _require_bf16(name, t)
+    elif H % 4:
+        raise ValueError(f"the fp32 expert path needs hidden % 4 == 0, got {H}")
     return T, H, k, E, I2 // 2
 
 
@@ -504,8 +583,84 @@ def experts_fwd(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate
     return _experts_fwd_kernels(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
 
 
+def _f32_gemm(A, B, offs, G, mode, M, N, K, sA, sB, sBg, C, sC, sCg, accumulate, s, tag):
+    """moe_f32_grouped_gemm: C(i, j) (+)= sum_r A(i, r) B(r, j), strides (sAi, sAr), (sBr, sBj), (sCi, sCj)."""
+    call("moe_f32_grouped_gemm", ptr(A), ptr(B), ptr(offs), G, mode, M, N, K, sA[0], sA[1], sB[0], sB[1], sBg, ptr(C),
+         sC[0], sC[1], sCg, int(accumulate), s, tag=tag)
+
+
+def _wgrad_launch(dc, a, offsets, E, S, n, k, dst, accumulate, tag):
+    """dW[g][n_, k_] = sum over group g's rows of dc[r, n_] a[r, k_] into dst [E, n, k]
+    (bf16 or fp32; added to it with ``accumulate``): the bf16 weight-gradient
+    GEMM, or for fp32 operands the fp32 grouped GEMM."""
+    s = _stream(dc)
+    if dc.dtype == torch.float32:
+        _f32_gemm(dc, a, offsets, E, 1, n, k, S, (1, n), (k, 1), 0, dst, (k, 1), n * k, accumulate, s, tag)
+    else:
+        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dst),
+             int(dst.dtype == torch.float32), int(accumulate), s, tag=tag)
+
+
+def _experts_fwd_f32(hidden, ids, w, gu, dn, T, H, k, E, I):
+    """The fp32 expert path (fp32 modules; TF integrations/moe.py:377-478 in fp32)."""
+    S = T * k
+    dev = hidden.device
+    s = _stream(hidden)
+    f32 = dict(dtype=torch.float32, device=dev)
+    xp = torch.empty(S, H, **f32)
+    perm = torch.empty(S, dtype=torch.int32, device=dev)
+    pos = torch.empty(S, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E, dtype=torch.int32, device=dev)
+    ws = _ws(_lib.load().moe_permute_workspace_bytes(S, E), dev)
+    # the row copy moves bytes: an fp32 row is 2H bf16-sized units
+    call("moe_permute_fwd", ptr(hidden), T, 2 * H, ptr(ids), k, 1, E, ptr(xp), ptr(perm), ptr(pos), ptr(counts),
+         ptr(offsets), ptr(ws), ws.numel(), s, tag="permute_fwd")
+    pre = torch.empty(S, 2 * I, **f32)
+    _f32_gemm(xp, gu, offsets, E, 0, S, 2 * I, H, (H, 1), (1, H), 2 * I * H, pre, (2 * I, 1), 0, False, s, "up_fwd")
+    act = torch.empty(S, I, **f32)
+    call("moe_f32_swiglu_fwd", ptr(pre), ptr(act), ptr(offsets), E, S, I, s, tag="up_fwd")
+    y = torch.empty(S, H, **f32)
+    _f32_gemm(act, dn, offsets, E, 0, S, H, I, (I, 1), (1, I), H * I, y, (H, 1), 0, False, s, "down_fwd")
+    out = torch.empty(T, H, **f32)
+    call("moe_f32_combine_fwd", ptr(y), ptr(pos), ptr(offsets), E, ptr(w), T, H, k, ptr(out), s, tag="combine_fwd")
+    return out, xp, pre, act, y, pos, offsets
+
+
+def _experts_bwd_f32(d_out, w, gu, dn, xp, pre, act, y, pos, offsets, wgrad, on_d_weights):
+    T, k = w.shape
+    E, I2, H = gu.shape
+    I = I2 // 2
+    S = T * k
+    dev = d_out.device
+    s = _stream(d_out)
+    f32 = dict(dtype=torch.float32, device=dev)
+    d_out = d_out.float().contiguous()
+    dy = torch.empty(S, H, **f32)
+    d_w = torch.empty(T, k, **f32)
+    call("moe_f32_combine_bwd", ptr(d_out), ptr(y), ptr(pos), ptr(offsets), E, ptr(w), T, H, k, ptr(dy), ptr(d_w), s,
+         tag="combine_bwd")
+    d_add = on_d_weights(d_w) if on_d_weights is not None else None
+    d_act = torch.empty(S, I, **f32)
+    _f32_gemm(dy, dn, offsets, E, 0, S, I, H, (H, 1), (I, 1), H * I, d_act, (I, 1), 0, False, s, "down_dgrad")
+    d_pre = torch.empty(S, 2 * I, **f32)
+    call("moe_f32_swiglu_bwd", ptr(d_act), ptr(pre), ptr(d_pre), ptr(offsets), E, S, I, s, tag="down_dgrad")
+    d_xp = torch.empty(S, H, **f32)
+    _f32_gemm(d_pre, gu, offsets, E, 0, S, H, 2 * I, (2 * I, 1), (H, 1), 2 * I * H, d_xp, (H, 1), 0, False, s,
+              "up_dgrad")
+    d_hidden = torch.empty(T, H, **f32)
+    call("moe_f32_permute_bwd", ptr(d_xp), ptr(pos), ptr(offsets), E, T, H, k, ptr(d_add), ptr(d_hidden), s,
+         tag="permute_bwd")
+    d_gu = wgrad("gate_up_proj", d_pre, xp, 2 * I, H)
+    d_down = wgrad("down_proj", dy, act, H, I)
+    return d_hidden, d_w, d_gu, d_down
+
+
 def _experts_fwd_kernels(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj):
     T, H, k, E, I = _check_experts(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj)
+    if hidden.dtype == torch.float32:
+        return _experts_fwd_f32(hidden.contiguous(), _ids64(top_k_index), top_k_weights.float().contiguous(),
+                                gate_up_proj.contiguous(), down_proj.contiguous(), T, H, k, E, I)
     S = T * k
     dev = hidden.device
     s = _stream(hidden)
@@ -553,6 +708,9 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     weights' gradient exists and returns a bf16 [T,H] gradient that the
     permute backward adds into d_hidden (the other path to the same input).
     Returns (d_hidden [T,H], d_weights [T,k] f32, wgrad's two results)."""
+    if xp.dtype == torch.float32:
+        return _experts_bwd_f32(d_out, top_k_weights.float().contiguous(), gate_up_proj, down_proj, xp, pre, act, y,
+                                pos_of_slot, offsets, wgrad, on_d_weights)
     T, k = top_k_weights.shape
     E, I2, H = gate_up_proj.shape
     I = I2 // 2
@@ -591,13 +749,11 @@ def experts_bwd(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down
     """(d_hidden [T,H], d_weights [T,k] f32, d_gate_up_proj, d_down_proj)."""
     E = gate_up_proj.shape[0]
     S = xp.shape[0]
-    s = _stream(d_out)
     params = {"gate_up_proj": gate_up_proj, "down_proj": down_proj}
 
     def wgrad(name, dc, a, n, k):
         dw = torch.empty_like(params[name])
-        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s,
-             tag="up_wgrad" if name == "gate_up_proj" else "down_wgrad")
+        _wgrad_launch(dc, a, offsets, E, S, n, k, dw, False, "up_wgrad" if name == "gate_up_proj" else "down_wgrad")
         return dw
 
     return experts_bwd_kernels(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets,
@@ -656,18 +812,16 @@ def experts_bwd_accumulate(d_out, top_k_weights, gate_up_proj, down_proj, xp, pr
     gradient of an accumulated projection is None."""
     E = gate_up_proj.shape[0]
     S = xp.shape[0]
-    s = _stream(d_out)
     params = {"gate_up_proj": (gate_up_proj, gu_grad), "down_proj": (down_proj, dn_grad)}
 
     def wgrad(name, dc, a, n, k):
         param, target = params[name]
         tag = "up_wgrad" if name == "gate_up_proj" else "down_wgrad"
-        if target is None:
+        if target is None or (dc.dtype == torch.float32 and target.dtype != torch.float32):
             dw = torch.empty_like(param)
-            call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s, tag=tag)
+            _wgrad_launch(dc, a, offsets, E, S, n, k, dw, False, tag)
             return dw
-        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(target),
-             int(target.dtype == torch.float32), 1, s, tag=tag)
+        _wgrad_launch(dc, a, offsets, E, S, n, k, target, True, tag)
         return None
 
     return experts_bwd_kernels(d_out, top_k_weights, gate_up_proj, down_proj, xp, pre, act, y, pos_of_slot, offsets,
@@ -743,10 +897,10 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
     if d_out is None and d_logits is None and d_scores is None and d_aux is None:
         return (None,) * 9
     targets = [_grad_target(p) for p in ctx.params] if ctx.params is not None else [None, None, None]
-    rw_target = targets[0] if targets[0] is not None and targets[0].dtype == BF16 else None
+    # the router's weight gradient is added in place into a .grad of its own dtype
+    rw_target = targets[0] if targets[0] is not None and targets[0].dtype == rw.dtype else None
     E = gu.shape[0]
     S = xp.shape[0]
-    s = _stream(x)
     grads = {}
 
     def router_backward(d_w):
@@ -763,12 +917,11 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
     def wgrad(name, dc, a, n, k):
         param, target = params[name]
         tag = "up_wgrad" if name == "gate_up_proj" else "down_wgrad"
-        if target is None:
+        if target is None or (dc.dtype == torch.float32 and target.dtype != torch.float32):
             dw = torch.empty_like(param)
-            call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(dw), 0, 0, s, tag=tag)
+            _wgrad_launch(dc, a, offsets, E, S, n, k, dw, False, tag)
             return dw
-        call("moe_grouped_gemm_wgrad", ptr(dc), ptr(a), ptr(offsets), E, S, n, k, ptr(target),
-             int(target.dtype == torch.float32), 1, s, tag=tag)
+        _wgrad_launch(dc, a, offsets, E, S, n, k, target, True, tag)
         return None
 
     if d_out is None:
