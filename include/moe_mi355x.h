@@ -60,7 +60,7 @@ int moe_router_logits_fwd(const void* x, const void* wr, float* logits,
                           int64_t T, int64_t H, int64_t E, void* stream);
 
 /* Fused router forward: logits = x · wrᵀ (+ logit_bias[E] when not NULL, f32),
- * then the top-k softmax of moe_router_topk_fwd.  For E <= 256 (a multiple
+ * then the top-k softmax of moe_router_topk_fwd.  For E <= 128 (a multiple
  * of 16) one kernel runs the GEMM, the reduction and the selection (no
  * workspace: the size query returns 0); otherwise the GEMM is split along H
  * into f32 partials held in the workspace and a second kernel reduces them

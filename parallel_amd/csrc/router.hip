@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "dma.h"
 #include "gemm.h"
 
 namespace moe {
@@ -313,16 +314,42 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
 }
 
 // The router GEMM, reduction, top-k softmax and aux partials in one pass, for
-// E <= 256 experts with E a multiple of 16.  A block takes the 16 tokens of
+// E <= 128 experts with E a multiple of 16.  A block takes the 16 tokens of
 // the 16-lane token layout (4 waves x 4 tokens).  Their logits
 // x[16 tokens, H] . wr[E, H]^T run on v_mfma_f32_16x16x32_bf16 (A: the token
 // rows, B: 16 experts; lane l holds row l % 16, k 8 (l / 16) .. + 7 of a
-// 32-deep k-step, and D row 4 (l / 16) + i, column l % 16), operands loaded
-// straight from memory: the block's x rows once, wr from L2.  Wave w sums
-// the k-steps w, w + 4, ...; the four wave partials are added in wave order
-// through LDS, and each token then goes through route_token as in
-// router_reduce_topk_kernel.  No split-K partials reach memory.
+// 32-deep k-step, and D row 4 (l / 16) + i, column l % 16).
+//
+// wr reaches LDS by DMA in 128-deep k-chunks: the chunk's 16 NPL wr rows
+// (256 bytes each; rows past E and k past H read as zeros) fill a ring stage
+// with 1 KiB instructions of 4 whole rows each.  Every block reads all of wr
+// from L2, so the DMA keeps every cache line it touches whole: loading the
+// MFMA operand layout straight from memory (16 rows x 64 bytes per
+// instruction) moved wr at a third of the rate.  x, read once from HBM, is
+// loaded straight into the A-operand registers, all of a wave's k-steps at
+// once (up to kFusedXSteps of them), so its HBM latency is paid once per
+// block rather than once per ring turn.  Wave w multiplies the 32-deep
+// k-step w of every chunk (k-steps w, w + 4, ...); the four wave partials
+// are added in wave order through LDS, and each token then goes through
+// route_token as in router_reduce_topk_kernel.  No split-K partials reach
+// memory.
+//
+// LDS layout of a stage: wr row e at e * 256 bytes, its 16-byte chunk c at
+// slot c ^ (e % 16), so that the 16 lanes of a ds_read_b128 pass (16 rows,
+// one chunk) touch all 64 banks.
 constexpr int kFusedTokens = 16;
+constexpr int kFusedChunk = 128;   // k per ring stage (one 32-deep k-step per wave)
+constexpr int kFusedXSteps = 32;   // x k-steps a wave holds in registers at once
+
+template <int NPL>
+struct FusedRing {
+  static constexpr int kRows = 16 * NPL;  // wr rows of a stage
+  static constexpr int kStageBytes = kRows * kFusedChunk * 2;
+  static constexpr int kStages = kStageBytes * 4 <= 160 * 1024 ? 4 : 3;  // E <= 128: 4
+  static constexpr int kInst = kStageBytes / 1024;  // DMA instructions per stage
+  static constexpr int kPerWave = kInst / kRouterWaves;
+  static_assert(kInst % kRouterWaves == 0, "a stage's DMA splits evenly over the waves");
+};
 
 template <int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
@@ -331,82 +358,118 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
     int64_t* __restrict__ indices, int T, int H, int E, int k_rt, int norm, const float* __restrict__ token_weight,
     float* __restrict__ aux_ws) {
   constexpr int LPT = 16;
-  constexpr int NE = NPL;          // 16-expert tiles covered (E <= 16 NPL)
-  constexpr int ROW = 16 * NE + 4;  // padded LDS row: the four 4-token row groups of a tile hit distinct banks
+  constexpr int NE = NPL;           // 16-expert tiles covered (E <= 16 NPL)
+  constexpr int ROW = 16 * NE + 4;  // padded row of the wave partials: the four 4-token row groups hit distinct banks
+  using R = FusedRing<NPL>;
+  constexpr int S = R::kStages, PW = R::kPerWave, XS = kFusedXSteps;
   static_assert(Tok<LPT>::kPerBlock == kFusedTokens, "a block's token slots are the MFMA tile's 16 rows");
+  static_assert((kRouterWaves * kFusedTokens * ROW + kFusedTokens * (2 * LPT * NPL + 1)) * 4 <= S * R::kStageBytes,
+                "the wave partials and the aux rows fit in the ring once it is drained");
   const int k = KT ? KT : k_rt;
-  __shared__ float wpart[kRouterWaves][kFusedTokens][ROW];
-  __shared__ float part[Tok<LPT>::kPerBlock][2 * LPT * NPL + 1];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(1024))) char ring[S * R::kStageBytes];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int t0 = blockIdx.x * kFusedTokens;
-  const int ne = E / 16;
-  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  constexpr uint32_t kOut = 0x80000000u;  // >= both resource sizes (checked on the host)
+  const u32x4_t rw = rsrc_words(wr, static_cast<uint32_t>(E) * static_cast<uint32_t>(H) * 2u);
+  const u32x4_t rx = rsrc_words(x, static_cast<uint32_t>(T) * static_cast<uint32_t>(H) * 2u);
+  // This wave's DMA instructions j < PW fill stage bytes 1024 (wave PW + j)
+  // onwards, wr rows 4 (wave PW + j) + lane / 16; per lane the row's byte
+  // offset (kOut for a row past E) and the k of its chunk within a k-chunk.
+  uint32_t dbase[PW];
+  int dk[PW];
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    const int r = 4 * (wave * PW + j) + lane / 16;
+    dk[j] = 8 * ((lane & 15) ^ (r & 15));
+    dbase[j] = r < E ? static_cast<uint32_t>(r) * static_cast<uint32_t>(H) * 2u : kOut;
+  }
+  const uint32_t ring_lds = lds_address(ring);
+  const int nch = (H + kFusedChunk - 1) / kFusedChunk;
+  auto issue = [&](int c, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      // H % 8 == 0: a lane's 8 k are all inside or all outside.  Past the
+      // last chunk kk >= H; a row past E stays out of range (kOut plus less
+      // than E H 2 bytes).
+      const int kk = c * kFusedChunk + dk[j];
+      const uint32_t off = kk < H ? dbase[j] + static_cast<uint32_t>(kk) * 2u : kOut;
+      dma16(rw, off, __builtin_amdgcn_readfirstlane(ring_lds + st * R::kStageBytes + (wave * PW + j) * 1024));
+    }
+  };
+  // A operand: x row t0 + l % 16, k 8 (l / 16) .. + 7 of k-step 4 c + wave.
+  const int r16 = lane & 15;
+  const bool t_ok = t0 + r16 < T;
+  const uint32_t xrow = static_cast<uint32_t>(t0 + r16) * static_cast<uint32_t>(H) * 2u;
+  auto x_off = [&](int c) __attribute__((always_inline)) {
+    const int kk = (4 * c + wave) * 32 + 8 * (lane >> 4);
+    return (t_ok && kk < H) ? xrow + static_cast<uint32_t>(kk) * 2u : kOut;
+  };
+  // B operand (tile n): wr row 16 n + l % 16, chunk 4 wave + l / 16.
+  const int frag = r16 * 256 + (((4 * wave + (lane >> 4)) ^ r16) << 4);
   f32x4_t acc[NE];
 #pragma unroll
   for (int n = 0; n < NE; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  // Operands come through buffer resources: an offset past a resource's end
-  // reads zeros, so rows past T or E and k past H need no branches, and the
-  // offsets are 32-bit.  A ring of D k-steps of operands sits in registers;
-  // a k-step's slot is refilled with the k-step D ahead right after its
-  // MFMAs are issued.
-  constexpr uint32_t kOut = 0x80000000u;  // >= both resource sizes (checked on the host)
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(x), 0, static_cast<int>(static_cast<uint32_t>(T) * H * 2u),
-                                        0x00020000);
-  const __amdgpu_buffer_rsrc_t rw =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(wr), 0, static_cast<int>(static_cast<uint32_t>(E) * H * 2u),
-                                        0x00020000);
-  const int nks = (H + 31) / 32;
-  const bool t_ok = t0 + r16 < T;
-  const uint32_t xrow = static_cast<uint32_t>(t0 + r16) * static_cast<uint32_t>(H) * 2u;
-  const uint32_t wrow = static_cast<uint32_t>(r16) * static_cast<uint32_t>(H) * 2u;
-  const uint32_t wtile = 16u * static_cast<uint32_t>(H) * 2u;  // bytes between 16-expert tiles
-  // x comes from HBM once, so a wave loads its x fragments for XC k-steps
-  // at once (one memory round trip per chunk); wr, read by every block, comes
-  // from L2 through a ring of D k-steps, refilled D ahead.  Within a chunk the
-  // code is straight-line, so the waits count exactly.
-  constexpr int XC = 16;               // k-steps per wave per chunk
-  constexpr int D = NE <= 8 ? 4 : 2;   // wr ring depth
-  static_assert(XC % D == 0, "the ring turns over whole chunks");
-  auto load16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) __attribute__((always_inline)) {
-    typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
-    const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-  };
-  auto kbytes = [&](int ks, bool& ok) __attribute__((always_inline)) {
-    const int kk = ks * 32 + kq;
-    ok = kk < H;  // H % 8 == 0: a lane's 8 k are all inside or all outside
-    return static_cast<uint32_t>(kk) * 2u;
-  };
-  uint4 rb[D][NE];
-  auto fetch_w = [&](int ks, uint4 (&b)[NE]) __attribute__((always_inline)) {
-    bool ok;
-    const uint32_t kb = kbytes(ks, ok);
+  // The multiply of k-chunk c reads its wr fragments one iteration ahead:
+  // iteration c waits for chunk c + 1 (this wave's DMA, all but the S - 3
+  // younger chunks, then every wave's through the barrier), refills the
+  // stage of chunk c - 1 (whose fragments were consumed by iteration c - 1's
+  // MFMAs, before the barrier) with chunk c + S - 1, reads chunk c + 1's
+  // fragments and multiplies chunk c's.
+  static_assert(S >= 3, "the fragment prefetch needs a stage between the one read and the one refilled");
+  bf16x8_t bq[NE];
+  for (int g0 = 0; g0 < nch; g0 += XS) {
+    // The x loads are inline assembly like the DMA, so that the compiler
+    // adds no waits of its own (it would count them without the DMA issued
+    // after them and drain the ring); each k-step's wait below names the
+    // register it makes ready.
+    u32x4_t xa[XS];
 #pragma unroll
-    for (int n = 0; n < NE; ++n)
-      b[n] = load16(rw, (n < ne && ok) ? wrow + static_cast<uint32_t>(n) * wtile + kb : kOut);
-  };
+    for (int q = 0; q < XS; ++q)
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen"
+                   : "=v"(xa[q])
+                   : "v"(g0 + q < nch ? x_off(g0 + q) : kOut), "s"(rx)
+                   : "memory");
+    if (g0 == 0) {
 #pragma unroll
-  for (int d = 0; d < D; ++d) fetch_w(wave + kRouterWaves * d, rb[d]);
-  for (int c0 = wave; c0 < nks; c0 += kRouterWaves * XC) {
-    uint4 xa[XC];
+      for (int s = 0; s < S - 1; ++s) issue(s, s);
+      wait_vmcnt<(S - 2) * PW>();  // chunk 0 (and the x loads before it)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
 #pragma unroll
-    for (int q = 0; q < XC; ++q) {
-      bool ok;
-      const uint32_t kb = kbytes(c0 + kRouterWaves * q, ok);
-      xa[q] = load16(rx, (t_ok && ok) ? xrow + kb : kOut);
+      for (int n = 0; n < NE; ++n) bq[n] = *reinterpret_cast<const bf16x8_t*>(ring + 16 * n * 256 + frag);
     }
 #pragma unroll
-    for (int q = 0; q < XC; ++q) {
-      const int d = q % D;
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa[q]);
-      // (tiles past E multiply the zeros their loads read)
+    for (int q = 0; q < XS; ++q) {
+      const int c = g0 + q;
+      if (c >= nch) break;
+      const int cst = c % S;
+      // The x loads of group 0 precede every DMA; a later group's follow the
+      // DMA of chunks up to g0 + S - 2, and at k-step q at least XS - 1 - q
+      // x loads and q PW DMA instructions are younger than xa[q], never fewer
+      // than the S - 3 chunks the wait leaves in flight: xa[q] is ready.
+      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(xa[q]) : "n"((S - 3) * PW) : "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(c + S - 1, cst == 0 ? S - 1 : cst - 1);
+      const char* nst = ring + (cst + 1 == S ? 0 : cst + 1) * R::kStageBytes;
+      bf16x8_t bn[NE];
 #pragma unroll
-      for (int n = 0; n < NE; ++n)
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, rb[d][n]), acc[n], 0, 0, 0);
-      fetch_w(c0 + kRouterWaves * (q + D), rb[d]);
+      for (int n = 0; n < NE; ++n) bn[n] = *reinterpret_cast<const bf16x8_t*>(nst + 16 * n * 256 + frag);
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa[q]);
+#pragma unroll
+      for (int n = 0; n < NE; ++n) {
+        // (tiles past E multiply the zeros their rows read)
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[n], acc[n], 0, 0, 0);
+        bq[n] = bn[n];
+      }
     }
   }
+  wait_vmcnt<0>();  // the trailing DMA (zeros) lands before the ring is reused
+  __syncthreads();
+  auto wpart = reinterpret_cast<float (*)[kFusedTokens][ROW]>(ring);
+  auto part = reinterpret_cast<float (*)[2 * LPT * NPL + 1]>(ring + kRouterWaves * kFusedTokens * ROW * 4);
 #pragma unroll
   for (int n = 0; n < NE; ++n)
 #pragma unroll
@@ -923,11 +986,13 @@ void router_split(int64_t T, int64_t H, int64_t E, int& splits, int& k_chunk) {
 }  // namespace
 
 namespace {
-// The one-pass router kernel covers up to 256 experts in 16-expert MFMA
-// tiles, with x and wr each under 2 GiB (its buffer resources).
+// The one-pass router kernel covers up to 128 experts in 16-expert MFMA
+// tiles (its wr ring holds three or four 128-deep k-chunks of every expert's
+// row), with x and wr each under 2 GiB (its buffer resources).
+constexpr int kFusedMaxExperts = 128;
 bool router_fused(int64_t T, int64_t H, int64_t E) {
   constexpr int64_t kMax = (1ll << 31) - 64;
-  return E <= 256 && E % 16 == 0 && T * H * 2 < kMax && E * H * 2 < kMax;
+  return E <= kFusedMaxExperts && E % 16 == 0 && T * H * 2 < kMax && E * H * 2 < kMax;
 }
 
 // logits, scores and indices of T >= 1 tokens and, with aux_ws, the aux
@@ -940,10 +1005,13 @@ int route_tokens(const void* x, const void* wr, const float* bias, float* logits
   const int blocks = token_blocks(T, E);
   if (router_fused(T, H, E)) {
     with_npl_k(E, k, [&](auto, auto N, auto K) {
-      hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
-                         dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
-                         static_cast<const bf16_t*>(wr), bias, logits, logits_b, scores, indices, static_cast<int>(T),
-                         static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm, token_weight, aux_ws);
+      if constexpr (16 * decltype(N)::value <= kFusedMaxExperts) {
+        hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
+                           dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
+                           static_cast<const bf16_t*>(wr), bias, logits, logits_b, scores, indices,
+                           static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm,
+                           token_weight, aux_ws);
+      }
     });
     return launch_status(name);
   }

@@ -1,13 +1,14 @@
-"""Hazard check of the GEMM's hand-issued LDS DMA in the generated gfx950 code.
+"""Hazard check of the hand-issued buffer loads in the generated gfx950 code.
 
-The DMA (``buffer_load_dwordx4 ... lds``) is issued from inline assembly, so
-the compiler's hazard recognizer does not protect it. gfx9 needs 5 wait
+The GEMM's and the router's LDS DMA (``buffer_load_dwordx4 ... lds``) and the
+router's x loads are issued from inline assembly, so the compiler's hazard
+recognizer does not protect them. gfx9 needs 5 wait
 states between a VALU write of an SGPR (``v_readfirstlane``, ``v_readlane``,
 ``v_cmp`` into an SGPR pair) and a VMEM instruction reading that SGPR. The
 buffer descriptor comes from such writes, and ``v_readlane`` also restores
 spilled SGPRs. A load that reads a stale descriptor base can fault. This test
-compiles the kernel source to assembly and checks every LDS DMA in every
-instantiation.
+compiles the kernel sources to assembly and checks every buffer load in every
+instantiation (the compiler's own loads pass by construction).
 """
 
 import re
@@ -18,7 +19,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-SRC = ROOT / "parallel_amd" / "csrc" / "grouped_gemm.hip"
+SRCS = [ROOT / "parallel_amd" / "csrc" / name for name in ("grouped_gemm.hip", "router.hip")]
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 _SGPR = re.compile(r"s\[(\d+):(\d+)\]|s(\d+)\b")
@@ -35,15 +36,16 @@ def _sgprs(text):
 
 
 def dma_hazards(asm_lines, window=5):
-    """(line, writer, load) triples where a VALU SGPR write precedes an LDS DMA
-    reading that SGPR by fewer than `window` wait states in straight-line code."""
+    """(line, writer, load) triples where a VALU SGPR write precedes a buffer
+    load reading that SGPR (its descriptor) by fewer than `window` wait states
+    in straight-line code."""
     found = []
     for n, line in enumerate(asm_lines):
         text = line.strip()
-        if not (text.startswith("buffer_load") and text.endswith(" lds")):
+        if not text.startswith("buffer_load"):
             continue
         operands = text.split(None, 1)[1].split(",")
-        rsrc = _sgprs(operands[1])
+        rsrc = next((_sgprs(o) for o in operands[1:] if o.strip().startswith("s")), set())
         waits, k = 0, n - 1
         while k >= 0 and waits < window:
             prev = asm_lines[k].strip()
@@ -75,15 +77,20 @@ def test_scanner_flags_a_planted_hazard():
     assert len(dma_hazards(planted)) == 1
     covered = ["v_readfirstlane_b32 s31, v4", "s_nop 4", "buffer_load_dwordx4 v9, s[28:31], 0 offen lds"]
     assert dma_hazards(covered) == []
+    # a load into registers: the descriptor is the first scalar operand
+    into_regs = ["v_readfirstlane_b32 s13, v4", "buffer_load_dwordx4 v[2:5], v2, s[12:15], 0 offen"]
+    assert len(dma_hazards(into_regs)) == 1
+    assert dma_hazards(["v_readfirstlane_b32 s13, v4", "s_nop 4", into_regs[1]]) == []
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
-def test_lds_dma_has_its_wait_states(tmp_path):
-    asm = tmp_path / "grouped_gemm.s"
+@pytest.mark.parametrize("src", SRCS, ids=lambda p: p.name)
+def test_lds_dma_has_its_wait_states(tmp_path, src):
+    asm = tmp_path / (src.stem + ".s")
     cmd = [
         HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-mcode-object-version=5",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "--cuda-device-only", "-S", str(SRC), "-o", str(asm),
+        "--cuda-device-only", "-S", str(src), "-o", str(asm),
     ]
     proc = subprocess.run(cmd, capture_output=True, text=True, cwd=ROOT)
     assert proc.returncode == 0, proc.stderr[-2000:]
