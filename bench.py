@@ -309,8 +309,9 @@ def units_summary(args, w, prof, cmd) -> None:
         f"# Expert-GEMM unit utilisation, workload {w.name} (per launch, averaged over the launches of each",
         "# entry point in the profiled run: warm-up, instrumented and timed steps)",
         "# commands (one counter set per pass):",
-        *[f"#   cd /tmp && rocprofv3 --pmc {c} -f csv -d <out>/{n} -o run -- python3 <repo>/bench.py --steps 2 "
-          f"--warmup 1 --no-cpu-baseline" for n, c in _UNIT_COUNTERS.items()],
+        *([f"#   {c}" for c in cmd.splitlines() if any(f"--pmc {v} " in c for v in _UNIT_COUNTERS.values())] or
+          [f"#   cd /tmp && rocprofv3 --pmc {c} -f csv -d <out>/{n} -o run -- python3 <repo>/bench.py --steps 2 "
+           f"--warmup 1 --no-cpu-baseline" for n, c in _UNIT_COUNTERS.items()]),
         *[f"#   {c}" for c in cmd.splitlines() if "--profile-summary" in c],
         "# Normalisation: GRBM_GUI_ACTIVE sums the 8 XCDs (per-XCD cycles = value / 8; with the kernel",
         "# durations this gives about 2.1 GHz); SQ_VMEM_TA_ADDR_FIFO_FULL and the TCP sums cover 256 CUs;",
