@@ -1146,14 +1146,16 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
 // k-step of LDS traffic, but with few output columns their grid (about one
 // or two m-tiles per expert times the column tiles) ends in a poorly
 // balanced last round; 384x128 tiles give one m-tile per expert of up to 384
-// rows and twice the column tiles.  When the experts average more than 384
-// rows (the many m-tiles per expert then balance the grid anyway) the
-// 256x256 tile's intensity wins: the down projection's input gradient at
-// 1024 rows per expert took 631 against 723 us on 384x128 tiles.
+// rows and twice the column tiles; they win when the experts hold about 256
+// rows each (a training step's uniform routing).  With more rows per expert
+// on average, or skewed counts, the 256x256 tile's intensity wins: the down
+// projection's input gradient took 631 against 723 us at 1024 rows per
+// expert (C4), 163 against 192 us at 380 rows with Zipf-skewed counts (C3).
 template <bool B_KCONTIG, int EPI>
 int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   const int out_cols = (EPI == EPI_SWIGLU_FWD) ? 2 * p.swiglu_I : p.N;
-  if (out_cols <= 1024 && static_cast<int64_t>(p.rows) <= static_cast<int64_t>(TallTile::BM) * p.G)
+  constexpr int64_t kTallMaxMeanRows = 288;
+  if (out_cols <= 1024 && static_cast<int64_t>(p.rows) <= kTallMaxMeanRows * p.G)
     return launch<MODE_MG, B_KCONTIG, EPI, TallTile>(p, stream, name);
   if constexpr (B_KCONTIG) return launch<MODE_MG, B_KCONTIG, EPI, BigTileP>(p, stream, name);
   return launch<MODE_MG, B_KCONTIG, EPI, BigTile>(p, stream, name);
