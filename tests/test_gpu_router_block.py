@@ -27,10 +27,12 @@ def gen(seed):
 
 # Every experts-per-lane width of the one-pass kernel (E = 16, 32, 64, 96/128),
 # H with a partial last k-step (72, 136, 264, 520), T not a multiple of the
-# block's 16 tokens; H above 4096 (4200, 8200) loads x in more than one group
-# of 32 k-steps per wave; E = 120 and E = 256 take the split-K path.
+# block's 16 tokens (1 and 17 leave most of a block's rows empty); H above
+# 4096 (4200, 8200) loads x in more than one group of 32 k-steps per wave;
+# E = 120 and E = 256 take the split-K path.
 ROUTER_CASES = [(257, 72, 16, 4), (300, 136, 32, 3), (1000, 520, 64, 6), (200, 264, 96, 5), (4096, 2048, 128, 8),
-                (70, 4200, 128, 8), (40, 8200, 48, 2), (129, 256, 256, 8), (300, 72, 120, 8)]
+                (70, 4200, 128, 8), (40, 8200, 48, 2), (1, 264, 128, 8), (17, 2048, 64, 4), (129, 256, 256, 8),
+                (300, 72, 120, 8)]
 
 
 @pytest.mark.parametrize("T,H,E,k", ROUTER_CASES)
