@@ -371,6 +371,52 @@ def cpu_baseline(w, tokens: int):
     }
 
 
+def calibration(w) -> dict:
+    """The box's own ceilings, measured after the timed region so that the
+    spec peaks the roofline quotes can be read against them: a 1 GiB
+    device-to-device copy (read + write bytes), hipBLASLt's dense bf16 GEMM
+    (torch.mm, 8192^3, the second operand K-contiguous as nn.Linear keeps
+    it) and its batched bf16 GEMM on the workload's up projection with the
+    routed rows split equally over the experts (torch.bmm, contiguous
+    operands: a transposed right operand is kept out of batched products).
+    Reference kernels, not this build's."""
+    import torch
+
+    dev = "cuda"
+
+    def timed(fn, reps=5):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    out = {}
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    dst = torch.empty_like(src)
+    out["torch_copy_gbs"] = round(2.0 * 4 * src.numel() / timed(lambda: dst.copy_(src)) / 1e9, 1)
+    del src, dst
+    n = 8192
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)  # [N, K], used as K-contiguous (nn.Linear's layout)
+    out["hipblaslt_dense_bf16_tflops"] = round(2.0 * n ** 3 / timed(lambda: torch.mm(a, b.t())) / 1e12, 1)
+    del a, b
+    E, H, I = (w.local_experts or w.experts), w.hidden, w.intermediate
+    rows = max(1, w.slots // E)
+    x = torch.randn(E, rows, H, device=dev, dtype=torch.bfloat16)
+    wt = torch.randn(E, H, 2 * I, device=dev, dtype=torch.bfloat16)  # contiguous [E, H, 2I]
+    out["hipblaslt_batched_up_bf16_tflops"] = round(2.0 * E * rows * H * 2 * I /
+                                                    timed(lambda: torch.bmm(x, wt)) / 1e12, 1)
+    out["batched_shape"] = f"{E} x [{rows} x {H}] . [{H} x {2 * I}]"
+    del x, wt
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure(w, steps: int, warmup: int, instrumented_steps: int):
     """Builds workload w's inputs on the GPU, runs `warmup` steps, an
     instrumented pass (events around every launch, outside the timed region)
@@ -617,6 +663,11 @@ def main() -> int:
             gc.collect()
             torch.cuda.empty_cache()
 
+    calib = None
+    if args.config == "c2" and not args.no_other_configs:
+        calib = calibration(w)
+        log(f"calibration: {calib}")
+
     cpu = None
     if not args.no_cpu_baseline and not w.local_experts:
         log(f"cpu baseline: {args.cpu_baseline_tokens} tokens on {torch.get_num_threads()} threads")
@@ -649,6 +700,8 @@ def main() -> int:
         "kernels_source": f"untimed instrumented pass of {args.instrumented_steps} steps (events around every launch)",
         "cpu_baseline": cpu,
     }
+    if calib:
+        result["calibration"] = calib
     if other:
         result["other_configs"] = other
         result["other_configs_note"] = ("C4 and C5 step times in the same run (value is C2's); grouped_gemm from "
