@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_reduce_topk_kerne
 // one chunk) touch all 64 banks.
 constexpr int kFusedTokens = 16;
 constexpr int kFusedChunk = 128;   // k per ring stage (one 32-deep k-step per wave)
-constexpr int kFusedXSteps = 32;   // x k-steps a wave holds in registers at once
+constexpr int kFusedXSteps = 32;   // x k-steps x row tiles a wave holds in registers at once
 
 template <int NPL>
 struct FusedRing {
@@ -351,7 +351,7 @@ struct FusedRing {
   static_assert(kInst % kRouterWaves == 0, "a stage's DMA splits evenly over the waves");
 };
 
-template <int NPL, int KT>
+template <int NPL, int KT, int MT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
     float* __restrict__ logits, bf16_t* __restrict__ logits_b, float* __restrict__ scores,
@@ -361,7 +361,10 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
   constexpr int NE = NPL;           // 16-expert tiles covered (E <= 16 NPL)
   constexpr int ROW = 16 * NE + 4;  // padded row of the wave partials: the four 4-token row groups hit distinct banks
   using R = FusedRing<NPL>;
-  constexpr int S = R::kStages, PW = R::kPerWave, XS = kFusedXSteps;
+  // Four row tiles of 128 experts hold 128 accumulator registers: the x
+  // group is halved there, or the compiler parks x registers in AGPRs while
+  // their loads are still in flight.
+  constexpr int S = R::kStages, PW = R::kPerWave, XS = kFusedXSteps / MT / (MT * NPL >= 32 ? 2 : 1);
   static_assert(Tok<LPT>::kPerBlock == kFusedTokens, "a block's token slots are the MFMA tile's 16 rows");
   static_assert((kRouterWaves * kFusedTokens * ROW + kFusedTokens * (2 * LPT * NPL + 1)) * 4 <= S * R::kStageBytes,
                 "the wave partials and the aux rows fit in the ring once it is drained");
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
   __shared__ __attribute__((aligned(1024))) char ring[S * R::kStageBytes];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int t0 = blockIdx.x * kFusedTokens;
+  const int t0 = blockIdx.x * kFusedTokens * MT;  // MT row tiles of 16 tokens
   constexpr uint32_t kOut = 0x80000000u;  // >= both resource sizes (checked on the host)
   const u32x4_t rw = rsrc_words(wr, static_cast<uint32_t>(E) * static_cast<uint32_t>(H) * 2u);
   const u32x4_t rx = rsrc_words(x, static_cast<uint32_t>(T) * static_cast<uint32_t>(H) * 2u);
@@ -397,19 +400,22 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
       dma16(rw, off, __builtin_amdgcn_readfirstlane(ring_lds + st * R::kStageBytes + (wave * PW + j) * 1024));
     }
   };
-  // A operand: x row t0 + l % 16, k 8 (l / 16) .. + 7 of k-step 4 c + wave.
+  // A operand of row tile m: x row t0 + 16 m + l % 16, k 8 (l / 16) .. + 7
+  // of k-step 4 c + wave.
   const int r16 = lane & 15;
-  const bool t_ok = t0 + r16 < T;
-  const uint32_t xrow = static_cast<uint32_t>(t0 + r16) * static_cast<uint32_t>(H) * 2u;
-  auto x_off = [&](int c) __attribute__((always_inline)) {
+  auto x_off = [&](int c, int m) __attribute__((always_inline)) {
+    const int t = t0 + 16 * m + r16;
     const int kk = (4 * c + wave) * 32 + 8 * (lane >> 4);
-    return (t_ok && kk < H) ? xrow + static_cast<uint32_t>(kk) * 2u : kOut;
+    return (t < T && kk < H) ? static_cast<uint32_t>(t) * static_cast<uint32_t>(H) * 2u + static_cast<uint32_t>(kk) * 2u
+                             : kOut;
   };
   // B operand (tile n): wr row 16 n + l % 16, chunk 4 wave + l / 16.
   const int frag = r16 * 256 + (((4 * wave + (lane >> 4)) ^ r16) << 4);
-  f32x4_t acc[NE];
+  f32x4_t acc[MT][NE];
 #pragma unroll
-  for (int n = 0; n < NE; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int n = 0; n < NE; ++n) acc[m][n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   // The multiply of k-chunk c reads its wr fragments one iteration ahead:
   // iteration c waits for chunk c + 1 (this wave's DMA, all but the S - 3
   // younger chunks, then every wave's through the barrier), refills the
@@ -417,19 +423,23 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
   // MFMAs, before the barrier) with chunk c + S - 1, reads chunk c + 1's
   // fragments and multiplies chunk c's.
   static_assert(S >= 3, "the fragment prefetch needs a stage between the one read and the one refilled");
+  static_assert((XS - 1) * MT >= (S - 3) * PW && XS >= S - 2,
+                "at every k-step the wait leaves in flight only loads younger than the step's x registers");
   bf16x8_t bq[NE];
   for (int g0 = 0; g0 < nch; g0 += XS) {
     // The x loads are inline assembly like the DMA, so that the compiler
     // adds no waits of its own (it would count them without the DMA issued
     // after them and drain the ring); each k-step's wait below names the
     // register it makes ready.
-    u32x4_t xa[XS];
+    u32x4_t xa[XS][MT];
 #pragma unroll
     for (int q = 0; q < XS; ++q)
-      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen"
-                   : "=v"(xa[q])
-                   : "v"(g0 + q < nch ? x_off(g0 + q) : kOut), "s"(rx)
-                   : "memory");
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen"
+                     : "=v"(xa[q][m])
+                     : "v"(g0 + q < nch ? x_off(g0 + q, m) : kOut), "s"(rx)
+                     : "memory");
     if (g0 == 0) {
 #pragma unroll
       for (int s = 0; s < S - 1; ++s) issue(s, s);
@@ -446,10 +456,13 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
       if (c >= nch) break;
       const int cst = c % S;
       // The x loads of group 0 precede every DMA; a later group's follow the
-      // DMA of chunks up to g0 + S - 2, and at k-step q at least XS - 1 - q
-      // x loads and q PW DMA instructions are younger than xa[q], never fewer
-      // than the S - 3 chunks the wait leaves in flight: xa[q] is ready.
-      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(xa[q]) : "n"((S - 3) * PW) : "memory");
+      // DMA of chunks up to g0 + S - 2, and at k-step q at least
+      // (XS - 1 - q) MT x loads and q PW DMA instructions are younger than
+      // xa[q][*], never fewer than the S - 3 chunks the wait leaves in
+      // flight: xa[q][*] are ready.
+      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(xa[q][0]) : "n"((S - 3) * PW) : "memory");
+#pragma unroll
+      for (int m = 1; m < MT; ++m) asm volatile("" : "+v"(xa[q][m]));
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       issue(c + S - 1, cst == 0 ? S - 1 : cst - 1);
@@ -457,41 +470,51 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
       bf16x8_t bn[NE];
 #pragma unroll
       for (int n = 0; n < NE; ++n) bn[n] = *reinterpret_cast<const bf16x8_t*>(nst + 16 * n * 256 + frag);
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa[q]);
 #pragma unroll
-      for (int n = 0; n < NE; ++n) {
-        // (tiles past E multiply the zeros their rows read)
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[n], acc[n], 0, 0, 0);
-        bq[n] = bn[n];
+      for (int m = 0; m < MT; ++m) {
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa[q][m]);
+#pragma unroll
+        for (int n = 0; n < NE; ++n)  // (tiles past E multiply the zeros their rows read)
+          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[n], acc[m][n], 0, 0, 0);
       }
+#pragma unroll
+      for (int n = 0; n < NE; ++n) bq[n] = bn[n];
     }
   }
   wait_vmcnt<0>();  // the trailing DMA (zeros) lands before the ring is reused
-  __syncthreads();
   auto wpart = reinterpret_cast<float (*)[kFusedTokens][ROW]>(ring);
   auto part = reinterpret_cast<float (*)[2 * LPT * NPL + 1]>(ring + kRouterWaves * kFusedTokens * ROW * 4);
-#pragma unroll
-  for (int n = 0; n < NE; ++n)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wpart[wave][4 * (lane >> 4) + i][16 * n + r16] = acc[n][i];
-  __syncthreads();
   const int sub = Tok<LPT>::sub(), slot = Tok<LPT>::slot();
-  const int t = t0 + slot;
-  float P[NPL], C[NPL];
+  const int rows = (T + kFusedTokens - 1) / kFusedTokens;  // aux partial rows: one per 16 tokens
+  // One row tile at a time through the wave partials: the barrier first
+  // retires the ring's last reads (m = 0) or the previous tile's reads of
+  // the partials and aux rows.
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
-  float W = 0.0f;
-  if (t < T) {
-    float v[NPL];
+  for (int m = 0; m < MT; ++m) {
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const int e = sub + j * LPT;
-      v[j] = ((wpart[0][slot][e] + wpart[1][slot][e]) + wpart[2][slot][e]) + wpart[3][slot][e];
+    for (int n = 0; n < NE; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wpart[wave][4 * (lane >> 4) + i][16 * n + r16] = acc[m][n][i];
+    __syncthreads();
+    const int t = t0 + 16 * m + slot;
+    float P[NPL], C[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) P[j] = C[j] = 0.0f;
+    float W = 0.0f;
+    if (t < T) {
+      float v[NPL];
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const int e = sub + j * LPT;
+        v[j] = ((wpart[0][slot][e] + wpart[1][slot][e]) + wpart[2][slot][e]) + wpart[3][slot][e];
+      }
+      route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, logits_b, scores, indices, token_weight,
+                                aux_ws != nullptr, P, C, W);
     }
-    route_token<LPT, NPL, KT>(v, t, E, k, norm, bias, logits, logits_b, scores, indices, token_weight,
-                              aux_ws != nullptr, P, C, W);
+    const int row = blockIdx.x * MT + m;  // block-uniform
+    if (aux_ws && row < rows) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(row) * (2 * E + 1));
   }
-  if (aux_ws) aux_block_partial<LPT>(part, P, C, W, E, aux_ws + static_cast<int64_t>(blockIdx.x) * (2 * E + 1));
 }
 
 // out[i] = bf16(sum_c partials[c][i]) over n elements, fixed order; with
@@ -1008,13 +1031,25 @@ int route_tokens(const void* x, const void* wr, const float* bias, float* logits
   bf16_t* logits_b = static_cast<bf16_t*>(logits_bf16);
   const int blocks = token_blocks(T, E);
   if (router_fused(T, H, E)) {
+    // Row tiles of 16 tokens per block: one while the blocks fit the CUs in
+    // one round, else two or four, so that a block's pass over wr (all of
+    // it, through L2) serves more tokens rather than the grid taking more
+    // rounds.
+    const int64_t cus = device_cus(current_device());
+    const int mt = blocks >= 4 * cus ? 4 : blocks >= 2 * cus ? 2 : 1;
+    const int grid = static_cast<int>((T + kFusedTokens * mt - 1) / (kFusedTokens * mt));
     with_npl_k(E, k, [&](auto, auto N, auto K) {
       if constexpr (16 * decltype(N)::value <= kFusedMaxExperts) {
-        hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value>), dim3(blocks),
-                           dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
-                           static_cast<const bf16_t*>(wr), bias, logits, logits_b, scores, indices,
-                           static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm,
-                           token_weight, aux_ws);
+        auto go = [&](auto M) {
+          hipLaunchKernelGGL((router_fused_fwd_kernel<decltype(N)::value, decltype(K)::value, decltype(M)::value>),
+                             dim3(grid), dim3(kRouterWaves * kWave), 0, st, static_cast<const bf16_t*>(x),
+                             static_cast<const bf16_t*>(wr), bias, logits, logits_b, scores, indices,
+                             static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), static_cast<int>(k), norm,
+                             token_weight, aux_ws);
+        };
+        if (mt == 4) go(std::integral_constant<int, 4>{});
+        else if (mt == 2) go(std::integral_constant<int, 2>{});
+        else go(std::integral_constant<int, 1>{});
       }
     });
     return launch_status(name);

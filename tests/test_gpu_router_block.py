@@ -32,7 +32,10 @@ def gen(seed):
 # E = 120 and E = 256 take the split-K path.
 ROUTER_CASES = [(257, 72, 16, 4), (300, 136, 32, 3), (1000, 520, 64, 6), (200, 264, 96, 5), (4096, 2048, 128, 8),
                 (70, 4200, 128, 8), (40, 8200, 48, 2), (1, 264, 128, 8), (17, 2048, 64, 4), (129, 256, 256, 8),
-                (300, 72, 120, 8)]
+                (300, 72, 120, 8),
+                # 8192+ and 16384+ tokens: two and four 16-token row tiles per block, ragged last block,
+                # one or two groups of x loads per block
+                (8200, 264, 64, 8), (8200, 2104, 64, 8), (16390, 1104, 128, 8), (16400, 72, 32, 4)]
 
 
 @pytest.mark.parametrize("T,H,E,k", ROUTER_CASES)
