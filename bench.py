@@ -8,10 +8,10 @@ HBM.  Prints one JSON line (metric, value, ..., roofline, cpu_baseline).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config c2]
 
-The dominant kernel's duration comes from HIP events recorded around each of
-its launches, on the stream the kernels run on, inside the timed region; no
-other launch in the timed region carries events (an event pair costs several
-microseconds of stream time).  The per-entry-point table comes from an
+The dominant kernel's duration comes from HIP events recorded around its
+launches, on the stream the kernels run on, inside the timed region, in every
+`--event-every`-th timed step (default 4); no other launch in the timed region
+carries events (an event pair costs several microseconds of stream time).  The per-entry-point table comes from an
 untimed instrumented pass (events around every launch) after the warm-up,
 which also picks the dominant kernel.  The CPU
 baseline times the reference's op sequence (F.grouped_mm on the CPU, the
@@ -417,11 +417,11 @@ def calibration(w) -> dict:
     return out
 
 
-def measure(w, steps: int, warmup: int, instrumented_steps: int):
+def measure(w, steps: int, warmup: int, instrumented_steps: int, event_every: int = 4):
     """Builds workload w's inputs on the GPU, runs `warmup` steps, an
     instrumented pass (events around every launch, outside the timed region)
     and `steps` timed steps in which only the dominant entry point carries
-    events.  Returns the step time, the per-entry-point durations and the
+    events, in every `event_every`-th step.  Returns the step time, the per-entry-point durations and the
     dominant entry point's launches in the timed region."""
     import torch
 
@@ -509,13 +509,15 @@ def measure(w, steps: int, warmup: int, instrumented_steps: int):
     durations = _lib.TIMER.durations_ms()
     dominant = max(durations, key=lambda t: sum(durations[t]))
 
-    # The timed region: only the dominant kernel's launches carry events.
+    # The timed region: only the dominant kernel's launches carry events, in
+    # every event_every-th step (each event pair leaves a gap of a few
+    # microseconds in the stream).
     _lib.TIMER.reset()
     _lib.TIMER.only = {dominant}
-    _lib.TIMER.enabled = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        _lib.TIMER.enabled = i % event_every == 0
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -537,6 +539,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2",
                     help="workload key (c1 c2 c3 c4 c5); c2 is the headline, c1 the reference's fp32 CPU case")
+    ap.add_argument("--event-every", type=int, default=4,
+                    help="timed steps per step whose dominant-kernel launches carry HIP events")
     ap.add_argument("--instrumented-steps", type=int, default=3,
                     help="untimed steps with events around every launch (the per-kernel table)")
     ap.add_argument("--cpu-baseline-tokens", type=int, default=4096)
@@ -589,7 +593,7 @@ def main() -> int:
     from parallel_amd.workloads import WORKLOADS, make_block_inputs
 
     w = WORKLOADS[args.config]
-    m = measure(w, args.steps, args.warmup, args.instrumented_steps)
+    m = measure(w, args.steps, args.warmup, args.instrumented_steps, max(1, args.event_every))
     ms_per_step, tokens_per_s, elapsed = m["ms_per_step"], m["tokens_per_s"], m["elapsed"]
     durations, dominant, dominant_ms, rows = m["durations"], m["dominant"], m["dominant_ms"], m["rows"]
 
@@ -627,6 +631,7 @@ def main() -> int:
     roofline["traffic"] = read_traffic(dominant, w.name)
     roofline["kernel"] = dominant
     roofline["avg_us_in_timed_region"] = round(avg_s * 1e6, 1)
+    roofline["launches_timed"] = len(m["dominant_ms"])
     roofline["algorithmic_bytes_per_launch"] = nbytes
     roofline["flops_per_launch"] = flops
     if flops is not None:
