@@ -204,6 +204,9 @@ def profile_summary(args) -> int:
     for tag, (total, calls) in sorted(per_tag.items(), key=lambda kv: -kv[1][0]):
         lines.append(f"avg_us_per_call {tag}: {total / calls:.1f}")
     (prof / f"kernel_stats_{w.name}.txt").write_text("\n".join(lines) + "\n")
+    if not (args.pmc_fetch and args.pmc_write and args.cal_fetch and args.cal_write):
+        log(f"wrote kernel_stats_{w.name}.txt under {prof} (no counter runs given)")
+        return 0
 
     # ---- HBM traffic
     def per_kernel(d, counter):
