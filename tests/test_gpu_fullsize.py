@@ -8,13 +8,17 @@ in seconds):
   schedules' multi-round tile loops, the even m-split of large experts and
   the cost split of the weight gradients at 128 experts, all at full size;
 * weight-gradient accumulation into existing gradients, fused in the kernel
-  against torch's separate add, bit for bit.
+  against torch's separate add, bit for bit;
+* the router at full size (one, two or four 16-token row tiles per block):
+  its logits against an fp32 torch product on the GPU, its routing against
+  the oracle's top-k on the returned logits, bit for bit.
 """
 
 import pytest
 import torch
 
-from conftest import close_bf16
+from conftest import close_bf16, routing_check
+from oracle import moe_oracle as O
 from parallel_amd import _lib, ops
 from parallel_amd.workloads import WORKLOADS, make_block_inputs
 
@@ -27,8 +31,23 @@ def _forward(w, seed):
     inp = make_block_inputs(w, seed=seed, device=DEV, dtype=BF, weights_on_device_rng=True)
     bias = inp.get("logit_bias")
     logits, scores, idx = ops.router_fwd(inp["x"], inp["router_weight"], w.top_k, w.norm_topk_prob, bias)
+    _check_router(inp, bias, logits, scores, idx, w)
     saved = ops.experts_fwd(inp["x"], idx, scores, inp["gate_up_proj"], inp["down_proj"])
     return inp, scores, idx, saved
+
+
+def _check_router(inp, bias, logits, scores, idx, w):
+    """Logits within fp32 accumulation-order noise of x.float() @ wr.float().T
+    (+ bias); indices and scores those of the oracle's softmax and top-k on
+    the returned logits (no exact ties on continuous random inputs)."""
+    ref = inp["x"].float() @ inp["router_weight"].float().t()
+    if bias is not None:
+        ref = ref + bias.float()
+    torch.testing.assert_close(logits, ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()))
+    lc = logits.cpu()
+    ref_s, ref_i = O.topk_softmax(lc, w.top_k, w.norm_topk_prob)
+    routing_check(idx, ref_i, lc)
+    torch.testing.assert_close(scores.cpu(), ref_s.float(), rtol=2e-6, atol=1e-7)
 
 
 def _dgrad(dc, wt, offsets, G, M, N, K):

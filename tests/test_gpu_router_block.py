@@ -125,7 +125,9 @@ def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
 
 
 @pytest.mark.parametrize("T,H,E,k,norm", [(1000, 256, 64, 6, True), (4096, 2048, 128, 8, True),
-                                          (300, 72, 120, 8, False), (257, 136, 32, 3, True)])
+                                          (300, 72, 120, 8, False), (257, 136, 32, 3, True),
+                                          # two and four 16-token row tiles per block
+                                          (8200, 2104, 64, 8, True), (16390, 1104, 128, 8, False)])
 def test_bf16_logit_router_routes_bit_exactly(T, H, E, k, norm):
     """Under the reference's bf16 autocast (parallel/parallel/engine/engine.py:141)
     Qwen3MoeTopKRouter's F.linear gives bf16 logits; softmax and top-k run in
