@@ -609,7 +609,19 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
       bool ok = id >= 0 && id < E;
       idx[r] = ok ? static_cast<int>(id) : -1;
       ds[r] = d_scores[static_cast<int64_t>(t) * k + r];
-      pv[r] = ok ? expf(row[idx[r]] - st.max) * inv_sum : 0.0f;
+      float lv;
+      if constexpr (LPT == kWave) {
+        // One token per wave: the selected logit is already in lane e % 64
+        // (v[e / 64]), fetched by readlane rather than a second load.
+        const int e = __builtin_amdgcn_readfirstlane(ok ? idx[r] : 0);
+        float cand = v[0];
+#pragma unroll
+        for (int j = 1; j < NPL; ++j) cand = (e / kWave == j) ? v[j] : cand;
+        lv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), e & (kWave - 1)));
+      } else {
+        lv = ok ? row[idx[r]] : 0.0f;
+      }
+      pv[r] = ok ? expf(lv - st.max) * inv_sum : 0.0f;
       tot += pv[r];
     }
   }
