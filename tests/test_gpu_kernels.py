@@ -375,7 +375,10 @@ def test_dgrad_swiglu_leaves_the_sentinel_tail_untouched():
 # ------------------------------------------------------------------- combine
 
 
-@pytest.mark.parametrize("T,k,E,H,sent", [(512, 2, 8, 256, 0.0), (1024, 8, 128, 2048, 0.0), (300, 4, 16, 72, 0.3)])
+# k spans the specialised (1, 2, 4, 6, 8) and the run-time (3, 16) slot counts.
+@pytest.mark.parametrize("T,k,E,H,sent", [(512, 2, 8, 256, 0.0), (1024, 8, 128, 2048, 0.0), (300, 4, 16, 72, 0.3),
+                                          (700, 3, 24, 136, 0.1), (64, 16, 32, 264, 0.0), (200, 6, 64, 72, 0.2),
+                                          (333, 1, 8, 520, 0.0)])
 def test_combine_forward_backward(T, k, E, H, sent):
     ids = _perm_case(T, k, E, 31, sentinel_frac=sent)
     hidden = torch.randn(T, H, generator=gen(32)).to(BF)
@@ -404,8 +407,9 @@ def test_combine_forward_backward(T, k, E, H, sent):
     close_bf16(d_s.view(T, k), ref_ds, "combine d_scores", max_rel=1e-3)
 
 
-def test_permute_backward_sums_routes():
-    T, k, E, H = 777, 4, 32, 136
+@pytest.mark.parametrize("k", [4, 5, 16])
+def test_permute_backward_sums_routes(k):
+    T, E, H = 777, 32, 136
     ids = _perm_case(T, k, E, 41, sentinel_frac=0.2)
     hidden = torch.zeros(T, H, dtype=BF, device=DEV)
     _, perm, pos, counts, offsets = ops.permute_fwd(hidden, ids.to(DEV), 1, E, False)
