@@ -270,6 +270,31 @@ def test_experts_concentrated_routing():
     assert not dl[2].grad[unused].any() and not dl[3].grad[unused].any(), "experts without routes get zero dW"
 
 
+@pytest.mark.parametrize("k", [3, 16])
+def test_experts_run_time_slot_count(k):
+    """The experts op at slot counts served by the run-time-k kernels (row
+    copy, combine, permute backward), forward and backward, against the
+    oracle's grouped experts."""
+    T, H, E, I = 257, 136, 24, 64
+    g = torch.Generator().manual_seed(23 + k)
+    x = torch.randn(T, H, generator=g).to(BF)
+    idx = torch.rand(T, E, generator=g).topk(k, dim=1).indices
+    scores = torch.softmax(torch.randn(T, k, generator=g), -1)
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(BF)
+    dn = (torch.randn(E, H, I, generator=g) * 0.05).to(BF)
+    d_out = torch.randn(T, H, generator=g).to(BF)
+    leaves = [t.clone().requires_grad_() for t in (x, scores, gu, dn)]
+    ref = O.experts_grouped(leaves[0], idx, leaves[1], leaves[2], leaves[3])
+    ref.backward(d_out)
+    dl = [t.to(DEV).requires_grad_() for t in (x, scores, gu, dn)]
+    out = ops.experts(dl[0], idx.to(DEV), dl[1], dl[2], dl[3])
+    out.backward(d_out.to(DEV))
+    torch.cuda.synchronize()
+    close_bf16(out, ref, f"k={k} out")
+    for name, a, b in zip(("dx", "d_scores", "d_gate_up", "d_down"), dl, leaves):
+        close_bf16(a.grad, b.grad, f"k={k} {name}")
+
+
 def test_empty_batch_through_router_and_experts():
     """A batch with no tokens (an EP rank can receive no rows): the reference's
     grouped experts return [0, H] and every weight gradient is zero.  Every
