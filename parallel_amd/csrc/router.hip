@@ -664,18 +664,20 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
 
 // ------------------------------------------------------------------ aux loss
 
-constexpr int kAuxBlocksMax = 1024;  // per-block partial rows (a token slot takes one token at a time)
-constexpr int kAuxGroups = 16;       // row groups of the partial reduction
+constexpr int kAuxGroups = 16;  // row groups of the partial reduction
 
 // Lanes per token for E experts, and tokens per block.
 constexpr int lanes_per_token(int64_t E) { return E <= 16 * kMaxPerLane ? 16 : kWave; }
 constexpr int tokens_per_block(int64_t E) { return kRouterWaves * (kWave / lanes_per_token(E)); }
 
+// One partial row per block of tokens_per_block(E) tokens, as the router
+// kernels write them, so that the standalone loss sums the same rows in the
+// same groups and gives their bits at any T.
 int aux_blocks(int64_t T, int64_t E) {
   const int64_t tpb = tokens_per_block(E);
   int64_t b = (T + tpb - 1) / tpb;
   if (b < 1) b = 1;
-  return static_cast<int>(b < kAuxBlocksMax ? b : kAuxBlocksMax);
+  return static_cast<int>(b);
 }
 
 // Per block partials: ws[b] = (P_0..P_{E-1}, c_0..c_{E-1}, W), fixed-order sums.
