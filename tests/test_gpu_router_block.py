@@ -36,7 +36,9 @@ ROUTER_CASES = [(257, 72, 16, 4), (300, 136, 32, 3), (1000, 520, 64, 6), (200, 2
                 # 8192+ and 16384+ tokens: two and four 16-token row tiles per block, ragged last block,
                 # one or two groups of x loads per block
                 (8200, 264, 64, 8), (8200, 2104, 64, 8), (16390, 1104, 128, 8), (16400, 72, 32, 4),
-                (16400, 264, 16, 2), (16390, 520, 64, 6)]
+                (16400, 264, 16, 2), (16390, 520, 64, 6),
+                # the split-K GEMM and reduce-and-select path at many tokens
+                (16400, 264, 120, 8), (9000, 136, 256, 8), (5000, 72, 320, 4)]
 
 
 @pytest.mark.parametrize("T,H,E,k", ROUTER_CASES)
