@@ -111,6 +111,23 @@ def test_moe_block_matches_the_separate_ops_and_the_oracle(base, tokens):
     close_bf16(blk["dx"], sep["dx"], f"{base} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
 
 
+@pytest.mark.parametrize("name", ["c2", "c4", "c5"])
+def test_moe_block_matches_the_separate_ops_at_full_size(name):
+    """The benchmark configurations at full size (C4 with its biased router,
+    C5 with its 4096-wide layer): moe_block gives the separate ops' bits for
+    the forward, the aux loss and every weight gradient."""
+    w = WORKLOADS[name]
+    inp = make_block_inputs(w, seed=14, device=DEV, dtype=BF, weights_on_device_rng=True)
+    bias = inp.get("logit_bias")
+    # each step gets its own leaves (tensors already on the device are not copied by .to)
+    blk = block_step(w, {key: t.clone() for key, t in inp.items()}, logit_bias=bias)
+    sep = gpu_block_step(w, {key: t.clone() for key, t in inp.items()}, logit_bias=bias)
+    torch.cuda.synchronize()
+    for key in ("logits", "scores", "indices", "out", "aux", "d_router", "d_gate_up", "d_down"):
+        assert torch.equal(blk[key], sep[key]), f"{name} {key}"
+    close_bf16(blk["dx"], sep["dx"], f"{name} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
+
+
 def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
     w = scaled(WORKLOADS["c2"], 512)
     inp = make_block_inputs(w, seed=12, dtype=BF)
