@@ -39,6 +39,7 @@ def block_inputs(T, H, E, I, seed):
 CASES = {
     "c1": dict(T=512, H=256, E=8, I=128, k=2),
     "ragged": dict(T=77, H=100, E=6, I=40, k=3),  # no dimension a multiple of the 32-row tile
+    "wide": dict(T=2048, H=1024, E=32, I=512, k=4),  # ~256 rows per expert, 1024- and 512-long reductions
 }
 
 
