@@ -112,12 +112,15 @@ def test_both_runtimes_give_the_same_share():
             close_bf16(x, y, f"ep {ep} rank {rank} {name}")
 
 
-@pytest.mark.parametrize("T,E,local,seed", [(512, 128, 16, 0), (1000, 64, 8, 1), (37, 16, 4, 2), (256, 8, 1, 3)])
-def test_dispatch_send_buffer_bit_exact(T, E, local, seed):
+@pytest.mark.parametrize("T,E,local,seed,k,H", [(512, 128, 16, 0, 4, 64), (1000, 64, 8, 1, 4, 64), (37, 16, 4, 2, 4, 64),
+                                                 (256, 8, 1, 3, 4, 64),
+                                                 # the C2 layer's send side at ep = 8 and ep = 2
+                                                 (4096, 128, 16, 4, 8, 2048), (4096, 128, 64, 5, 8, 2048)])
+def test_dispatch_send_buffer_bit_exact(T, E, local, seed, k, H):
     """ops.dispatch_fwd at ep = E / local equals TokenDispatcher.dispatch's send
     side (the oracle's restatement) bit for bit: rows, local expert ids,
     scores, source tokens and splits."""
-    H, k = 64, 4 if E >= 4 else E
+    k = min(k, E)
     g = torch.Generator().manual_seed(seed)
     hidden = torch.randn(T, H, generator=g).to(BF)
     idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
