@@ -60,7 +60,8 @@ def test_rmsnorm_shapes_against_oracle(T, H):
 
 
 @pytest.mark.parametrize("T,H,E,k,masked,biased", [(4096, 2048, 128, 8, False, False), (300, 64, 64, 6, True, True),
-                                                   (4, 8, 8, 2, False, False)])
+                                                   (4, 8, 8, 2, False, False), (16400, 2048, 128, 8, True, True),
+                                                   (8200, 4096, 128, 8, False, True)])
 def test_router_aux_equals_router_then_aux(T, H, E, k, masked, biased):
     """One pass (router top-k + aux partials) = router_fwd then aux_loss_fwd, bit for bit."""
     g = gen(T + E)
@@ -76,8 +77,8 @@ def test_router_aux_equals_router_then_aux(T, H, E, k, masked, biased):
     assert torch.equal(aux, a2) and torch.equal(stats, st2)
 
 
-def test_norm_router_aux_forward_backward_against_oracle():
-    T, H, E, k = 512, 256, 32, 4
+@pytest.mark.parametrize("T,H,E,k", [(512, 256, 32, 4), (4096, 2048, 128, 8)])
+def test_norm_router_aux_forward_backward_against_oracle(T, H, E, k):
     g = gen(77)
     hidden = (torch.randn(2, T // 2, H, generator=g) * 2).to(BF)
     nw = (1 + 0.1 * torch.randn(H, generator=g)).to(BF)
