@@ -34,9 +34,11 @@ def _layout(E, H, I, world):
         [("gate_up_proj", (E, 2 * I, H)), ("router", (E, H)), ("down_proj", (E, H, I))], world)
 
 
-@pytest.mark.parametrize("world", [1, 2, 3, 4])
-def test_bucket_matches_packed_dense_gradients(world):
-    T, H, E, k, I = 96, 256, 6, 2, 128
+@pytest.mark.parametrize("world,T,H,E,k,I", [(1, 96, 256, 6, 2, 128), (2, 96, 256, 6, 2, 128), (3, 96, 256, 6, 2, 128),
+                                              (4, 96, 256, 6, 2, 128),
+                                              # the C2 layer: 16 experts per rank, and 43 with a padded last chunk
+                                              (8, 4096, 2048, 128, 8, 768), (3, 4096, 2048, 128, 8, 768)])
+def test_bucket_matches_packed_dense_gradients(world, T, H, E, k, I):
     x, idx, scores, gu, dn, d_out = _inputs(T, H, E, k, I, seed=world)
     out, *saved = ops.experts_fwd(x, idx, scores, gu, dn)
     d_x, d_w, d_gu, d_dn = ops.experts_bwd(d_out, scores, gu, dn, *saved)
