@@ -70,11 +70,11 @@ def close_on_device(actual, expected, name, max_rel=2e-2, min_cos=0.9999):
     return rel
 
 
-@pytest.mark.parametrize("name,seed", [("c2", 31), ("c4", 32), ("c5", 33)])
-def test_full_size_backward_every_expert(name, seed):
-    w = WORKLOADS[name]
+def _backward_checks(name, w, inp, scores, saved, seed):
+    """Runs the experts' backward on saved forward state and checks every
+    expert's dW and input gradients against per-expert fp32 products of the
+    kernels' own inputs; returns the per-expert row counts."""
     E, H, I, S = w.experts, w.hidden, w.intermediate, w.slots
-    inp, scores, idx, saved = _forward(w, seed)
     out, xp, pre, act, y, pos, offsets = saved
     d_out = torch.randn(w.tokens, H, generator=torch.Generator(device=DEV).manual_seed(seed), device=DEV).to(BF)
     captured = {}
@@ -97,7 +97,6 @@ def test_full_size_backward_every_expert(name, seed):
     off = offsets.cpu().long().tolist()
     assert off[-1] == S
     counts = [off[0]] + [off[e] - off[e - 1] for e in range(1, E)]
-    assert max(counts) > 256, "some expert must span several m-tiles"
     worst = {}
     r0 = 0
     for e in range(E):
@@ -115,6 +114,30 @@ def test_full_size_backward_every_expert(name, seed):
         r0 = r1
     print(f"{name}: worst normwise max rel err per product over {E} experts: {worst}")
     assert torch.isfinite(d_hidden.float()).all() and torch.isfinite(d_w).all()
+    return counts
+
+
+@pytest.mark.parametrize("name,seed", [("c2", 31), ("c4", 32), ("c5", 33)])
+def test_full_size_backward_every_expert(name, seed):
+    w = WORKLOADS[name]
+    inp, scores, idx, saved = _forward(w, seed)
+    counts = _backward_checks(name, w, inp, scores, saved, seed)
+    assert max(counts) > 256, "some expert must span several m-tiles"
+
+
+def test_full_size_concentrated_routing():
+    """C4's 16384 tokens all routed to the same 8 experts: 16384 rows each
+    (64 evenly split m-tiles), 120 empty experts, and the weight gradients'
+    cost split with nearly all the cost in 8 groups."""
+    w = WORKLOADS["c4"]
+    inp = make_block_inputs(w, seed=51, device=DEV, dtype=BF, weights_on_device_rng=True)
+    g = torch.Generator(device=DEV).manual_seed(52)
+    chosen = torch.tensor([3, 17, 40, 41, 77, 90, 101, 127], device=DEV)
+    idx = chosen.repeat(w.tokens, 1)
+    scores = torch.softmax(torch.randn(w.tokens, w.top_k, generator=g, device=DEV), -1)
+    saved = ops.experts_fwd(inp["x"], idx, scores, inp["gate_up_proj"], inp["down_proj"])
+    counts = _backward_checks("c4 concentrated", w, inp, scores, saved, 53)
+    assert sorted(c for c in counts if c) == [w.tokens] * 8 and counts.count(0) == w.experts - 8
 
 
 def test_full_c4_gradient_accumulation_fused_equals_torch_add():
