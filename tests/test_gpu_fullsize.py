@@ -2,9 +2,10 @@
 through size-independent properties (the CPU oracle cannot run these sizes
 in seconds):
 
-* every expert's weight gradients and input gradients against plain fp32
-  torch.mm references of the same products, computed per expert on the GPU
-  from the kernels' own inputs (d_pre and xp, dy and act): the persistent
+* every expert's forward products (pre-activations, down projection) and
+  weight and input gradients against plain fp32 torch.mm references of the
+  same products, computed per expert on the GPU from the kernels' own inputs
+  (xp, act, d_pre, dy), the SwiGLU and the weighted combine: the persistent
   schedules' multi-round tile loops, the even m-split of large experts and
   the cost split of the weight gradients at 128 experts, all at full size;
 * weight-gradient accumulation into existing gradients, fused in the kernel
@@ -71,11 +72,19 @@ def close_on_device(actual, expected, name, max_rel=2e-2, min_cos=0.9999):
 
 
 def _backward_checks(name, w, inp, scores, saved, seed):
-    """Runs the experts' backward on saved forward state and checks every
-    expert's dW and input gradients against per-expert fp32 products of the
-    kernels' own inputs; returns the per-expert row counts."""
+    """Checks the saved forward state (SwiGLU, combine, every expert's up and
+    down products), runs the experts' backward on it and checks every
+    expert's dW and input gradients, against fp32 products of the kernels'
+    own inputs; returns the per-expert row counts."""
     E, H, I, S = w.experts, w.hidden, w.intermediate, w.slots
     out, xp, pre, act, y, pos, offsets = saved
+    # forward: the SwiGLU of the saved pre-activations (gate | up) and the
+    # weighted combine of the down projection's rows
+    g_, u_ = pre.float()[:, :I], pre.float()[:, I:]
+    close_on_device(act, torch.nn.functional.silu(g_) * u_, f"{name} act")
+    T, k = w.tokens, w.top_k
+    posl = pos.long().view(T, k)
+    close_on_device(out, (y.float()[posl] * scores.float().unsqueeze(-1)).sum(1), f"{name} out")
     d_out = torch.randn(w.tokens, H, generator=torch.Generator(device=DEV).manual_seed(seed), device=DEV).to(BF)
     captured = {}
 
@@ -106,7 +115,8 @@ def _backward_checks(name, w, inp, scores, saved, seed):
             assert not d_gu[e].any() and not d_dn[e].any(), f"{name} expert {e}: empty expert needs zero dW"
         else:
             f = lambda t: t[rows].float()  # noqa: E731
-            checks = (("d_gate_up", d_gu[e], f(d_pre).t() @ f(xp)), ("d_down", d_dn[e], f(dy).t() @ f(act)),
+            checks = (("pre", pre[rows], f(xp) @ gu[e].float().t()), ("y", y[rows], f(act) @ dn[e].float().t()),
+                      ("d_gate_up", d_gu[e], f(d_pre).t() @ f(xp)), ("d_down", d_dn[e], f(dy).t() @ f(act)),
                       ("d_xp", d_xp[rows], f(d_pre) @ gu[e].float()), ("d_act", d_act[rows], f(dy) @ dn[e].float()))
             for label, got, ref in checks:
                 rel = close_on_device(got, ref, f"{name} expert {e} ({r1 - r0} rows) {label}")
