@@ -1048,11 +1048,13 @@ int route_tokens(const void* x, const void* wr, const float* bias, float* logits
   const int blocks = token_blocks(T, E);
   if (router_fused(T, H, E)) {
     // Row tiles of 16 tokens per block: one while the blocks fit the CUs in
-    // one round, else two or four, so that a block's pass over wr (all of
-    // it, through L2) serves more tokens rather than the grid taking more
-    // rounds.
+    // one round, else two (up to twice the CUs) or four, so that a block's
+    // pass over wr (all of it, through L2) serves more tokens rather than
+    // the grid taking more rounds.  On 256 CUs, H 2048: 5000-8000 tokens
+    // 37 -> 27 us with two tiles, 10000-16000 tokens 53-56 -> 45-46 us with
+    // four instead of two.
     const int64_t cus = device_cus(current_device());
-    const int mt = blocks >= 4 * cus ? 4 : blocks >= 2 * cus ? 2 : 1;
+    const int mt = blocks > 2 * cus ? 4 : blocks > cus ? 2 : 1;
     const int grid = static_cast<int>((T + kFusedTokens * mt - 1) / (kFusedTokens * mt));
     with_npl_k(E, k, [&](auto, auto N, auto K) {
       if constexpr (16 * decltype(N)::value <= kFusedMaxExperts) {

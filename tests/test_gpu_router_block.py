@@ -33,9 +33,10 @@ def gen(seed):
 ROUTER_CASES = [(257, 72, 16, 4), (300, 136, 32, 3), (1000, 520, 64, 6), (200, 264, 96, 5), (4096, 2048, 128, 8),
                 (70, 4200, 128, 8), (40, 8200, 48, 2), (1, 264, 128, 8), (17, 2048, 64, 4), (129, 256, 256, 8),
                 (300, 72, 120, 8),
-                # 8192+ and 16384+ tokens: two and four 16-token row tiles per block, ragged last block,
-                # one or two groups of x loads per block
-                (8200, 264, 64, 8), (8200, 2104, 64, 8), (16390, 1104, 128, 8), (16400, 72, 32, 4),
+                # past 4096 and 8192 tokens (256 CUs): two and four 16-token row tiles per block,
+                # ragged last block, one or several groups of x loads per block
+                (5000, 264, 128, 8), (6000, 2104, 64, 8), (8200, 264, 64, 8), (8200, 2104, 64, 8),
+                (16390, 1104, 128, 8), (16400, 72, 32, 4),
                 (16400, 264, 16, 2), (16390, 520, 64, 6),
                 # the split-K GEMM and reduce-and-select path at many tokens
                 (16400, 264, 120, 8), (9000, 136, 256, 8), (5000, 72, 320, 4)]
@@ -147,7 +148,8 @@ def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
 @pytest.mark.parametrize("T,H,E,k,norm", [(1000, 256, 64, 6, True), (4096, 2048, 128, 8, True),
                                           (300, 72, 120, 8, False), (257, 136, 32, 3, True),
                                           # two and four 16-token row tiles per block
-                                          (8200, 2104, 64, 8, True), (16390, 1104, 128, 8, False)])
+                                          (6000, 2104, 64, 8, True), (8200, 2104, 64, 8, True),
+                                          (16390, 1104, 128, 8, False)])
 def test_bf16_logit_router_routes_bit_exactly(T, H, E, k, norm):
     """Under the reference's bf16 autocast (parallel/parallel/engine/engine.py:141)
     Qwen3MoeTopKRouter's F.linear gives bf16 logits; softmax and top-k run in
