@@ -123,7 +123,10 @@ def _backward_checks(name, w, inp, scores, saved, seed):
                 worst[label] = max(worst.get(label, 0.0), rel)
         r0 = r1
     print(f"{name}: worst normwise max rel err per product over {E} experts: {worst}")
-    assert torch.isfinite(d_hidden.float()).all() and torch.isfinite(d_w).all()
+    # the combine backward's score gradient <d_out[t], y[pos(t, j)]> and the
+    # permute backward's sum of each token's k input-gradient rows
+    close_on_device(d_w.view(T, k), (y.float()[posl] * d_out.float().unsqueeze(1)).sum(-1), f"{name} d_scores")
+    close_on_device(d_hidden, d_xp.float()[posl].sum(1), f"{name} d_hidden")
     return counts
 
 
