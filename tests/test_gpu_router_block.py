@@ -129,6 +129,23 @@ def test_moe_block_matches_the_separate_ops_at_full_size(name):
     close_bf16(blk["dx"], sep["dx"], f"{name} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
 
 
+def test_moe_block_on_a_side_stream_gives_the_default_stream_bits():
+    """Every launch goes to torch's current stream: the block's forward and
+    backward issued on another stream (default priority) give the same bits
+    as on the default stream."""
+    w = scaled(WORKLOADS["c2"], 1024)
+    inp = make_block_inputs(w, seed=15, dtype=BF)
+    ref = block_step(w, inp)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        got = block_step(w, inp)
+    torch.cuda.synchronize()
+    for key in ("logits", "scores", "indices", "out", "aux", "dx", "d_router", "d_gate_up", "d_down"):
+        assert torch.equal(got[key], ref[key]), key
+
+
 def test_moe_block_accumulates_every_weight_gradient_in_the_kernels():
     w = scaled(WORKLOADS["c2"], 512)
     inp = make_block_inputs(w, seed=12, dtype=BF)
