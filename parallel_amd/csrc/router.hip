@@ -363,7 +363,8 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_fused_fwd_kernel(
   using R = FusedRing<NPL>;
   // Four row tiles of 128 experts hold 128 accumulator registers: the x
   // group is halved there, or the compiler parks x registers in AGPRs while
-  // their loads are still in flight.
+  // their loads are still in flight (tests/test_asm_hazards.py checks every
+  // instantiation's assembly for such early uses).
   constexpr int S = R::kStages, PW = R::kPerWave, XS = kFusedXSteps / MT / (MT * NPL >= 32 ? 2 : 1);
   static_assert(Tok<LPT>::kPerBlock == kFusedTokens, "a block's token slots are the MFMA tile's 16 rows");
   static_assert((kRouterWaves * kFusedTokens * ROW + kFusedTokens * (2 * LPT * NPL + 1)) * 4 <= S * R::kStageBytes,
