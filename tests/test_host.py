@@ -44,12 +44,12 @@ def test_library_exports_every_declared_symbol():
 def test_library_size_queries_and_argument_checks_run_without_a_gpu():
     lib = _lib.load()
     assert lib.moe_permute_workspace_bytes(32768, 128) == 64 * 129 * 4  # 512-route chunks x (E + sentinel)
-    # one partial row per block (16 tokens for E <= 256, else 4; at most 1024 rows)
-    # plus 16 row-group sums, each 2E+1 floats
+    # one partial row per block (16 tokens for E <= 256, else 4), as the router
+    # kernels write them, plus 16 row-group sums, each 2E+1 floats
     assert lib.moe_aux_loss_workspace_bytes(4096, 128) == (256 + 16) * 257 * 4
     assert lib.moe_aux_loss_workspace_bytes(40, 8) == (3 + 16) * 17 * 4
     assert lib.moe_aux_loss_workspace_bytes(4096, 512) == (1024 + 16) * 1025 * 4
-    assert lib.moe_aux_loss_workspace_bytes(1 << 20, 128) == (1024 + 16) * 257 * 4
+    assert lib.moe_aux_loss_workspace_bytes(1 << 20, 128) == (65536 + 16) * 257 * 4
     # one pass for E <= 256 in 16-expert tiles (no split-K partials), split-K otherwise
     assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 128) == 0
     assert lib.moe_router_fwd_workspace_bytes(4096, 2048, 120) >= 4096 * 120 * 4
