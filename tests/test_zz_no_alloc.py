@@ -53,6 +53,36 @@ def test_noalloc_permute_equals_permute_on_consecutive_calls():
         assert not got[0][int(want[4][-1]):].any()
 
 
+@pytest.mark.gpu
+def test_noalloc_permute_at_its_largest_size():
+    """The largest size the scratch takes at 128 buckets: 2032 chunks of 512
+    routes (1,048,512 of its 1,048,576 bytes), routing only (no rows)."""
+    lib = _lib.load()
+    T, k, nb = 130048, 8, 128
+    assert lib.moe_permute_workspace_bytes(T * k, nb) == 2032 * 129 * 4
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, nb + 1, (T, k), generator=g).to(DEV)
+    S = T * k
+    outs = {}
+    for name in ("moe_permute_fwd", "moe_permute_fwd_noalloc"):
+        i32 = dict(dtype=torch.int32, device=DEV)
+        perm, pos, counts, offsets = (torch.empty(S, **i32), torch.empty(S, **i32), torch.empty(nb, **i32),
+                                      torch.empty(nb, **i32))
+        common = (None, T, 8, ids.data_ptr(), k, 1, nb, None, perm.data_ptr(), pos.data_ptr(), counts.data_ptr(),
+                  offsets.data_ptr())
+        stream = _lib.stream_of(ids)
+        if name == "moe_permute_fwd":
+            ws = torch.empty(lib.moe_permute_workspace_bytes(S, nb), dtype=torch.uint8, device=DEV)
+            _lib.check(lib.moe_permute_fwd(*common, ws.data_ptr(), ws.numel(), stream), name)
+        else:
+            _lib.check(lib.moe_permute_fwd_noalloc(*common, stream), name)
+        outs[name] = (perm, pos, counts, offsets)
+    torch.cuda.synchronize()
+    for label, a, b in zip(("perm", "pos_of_slot", "counts", "offsets"), outs["moe_permute_fwd_noalloc"],
+                           outs["moe_permute_fwd"]):
+        assert torch.equal(a, b), label
+
+
 def test_noalloc_permute_refuses_sizes_beyond_its_scratch():
     """Host-side check only: no HIP call happens for a refused size."""
     lib = _lib.load()
