@@ -182,9 +182,14 @@ __device__ int2 kg_cost_split(const int32_t* offs, int G, int rows, int per_grou
 }
 
 // Tile configurations: BK-deep k-tiles staged through a STAGES-deep LDS ring.
-// PIPE selects the software-pipelined k-loop of the one-wave-per-SIMD
-// layouts (each wave reads the next 16-deep half step's fragments while its
-// MFMAs run; one barrier per k-step, between the halves).
+// PIPE selects the k-loop:
+//   0  every wave reads its fragments, multiplies and fires its share of the
+//      DMA in each k-step (block barrier every second k-step);
+//   1  the same with the next 16-deep half step's fragments read while the
+//      current half step's MFMAs run (one barrier per k-step);
+//   2  ping-pong: the two waves of a SIMD take turns, one multiplying a k-step
+//      from registers while the other reads the next k-step's fragments and
+//      fires DMA (two barriers per k-step).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int PIPE_ = 0>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_, PIPE = PIPE_;
@@ -198,15 +203,12 @@ using BigTile = TileCfg<256, 256, 32, 2, 4, 5>;
 using TallTile = TileCfg<384, 128, 32, 4, 2, 5>;
 // Router GEMMs (N = E = 128): 80 KiB ring, 4 waves (two workgroups per CU).
 using SmallTile = TileCfg<128, 128, 32, 2, 2, 5>;
-// Expert GEMMs, one wave per SIMD: 128x128 wave tiles (16 accumulator
-// sub-tiles, 256 fp32 registers per lane), so a k-step reads 64 KiB of
-// fragments from LDS per CU instead of the 96 KiB of 128x64 wave tiles; with
-// the 32 KiB of DMA writes that is 96 of the 128 bytes per clock the LDS
-// serves at the MFMA peak, where eight 128x64 waves would need all 128.
-using BigTile4 = TileCfg<256, 256, 32, 2, 2, 5, 1>;
-// The same loop on eight 128x64 waves (two per SIMD).
+// The 256x256 loop with the fragment reads of each 16-deep half step
+// overlapping the previous half step's MFMAs.
 using BigTileP = TileCfg<256, 256, 32, 2, 4, 5, 1>;
-using TallTileP = TileCfg<384, 128, 32, 4, 2, 5, 1>;
+// Ping-pong on 256x256 tiles: waves 0-3 (one per SIMD) own output columns
+// 0-127, waves 4-7 columns 128-255; wave w and wave w + 4 share a SIMD.
+using PingTile = TileCfg<256, 256, 32, 2, 4, 5, 2>;
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -300,8 +302,11 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
-  constexpr int LPW_A = NI_A / NWAVES, LPW_B = NI_B / NWAVES;  // ... per wave and operand
-  constexpr int LPW = LPW_A + LPW_B;
+  // Ping-pong: the DMA of a k-tile is split by operand between the wave
+  // groups (waves 0-3 fire A, waves 4-7 fire B), LPW instructions per wave.
+  constexpr bool PING = CFG::PIPE == 2;
+  constexpr int LPW_A = PING ? 0 : NI_A / NWAVES, LPW_B = PING ? 0 : NI_B / NWAVES;  // ... per wave and operand
+  constexpr int LPW = PING ? NI_A / 4 : LPW_A + LPW_B;
   // Barrier cadence.  With a 5-deep ring the DMA runs LEAD = 3 k-steps ahead
   // and the block synchronises on even k-steps only: an even step waits for
   // its own k-tile and the next one, and the DMA of any step targets the
@@ -319,20 +324,27 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // middle of iteration c - 1, and both halves of iteration c come after that
   // barrier.  The DMA younger than the k-tile waited for is k-tile c + 2 and
   // the first half of c + 3.
-  constexpr bool PIPE = CFG::PIPE != 0;
-  constexpr bool PAIR = STAGES == 5 && !PIPE;
-  constexpr int LEAD = (PAIR || PIPE) ? STAGES - 2 : STAGES - 1;
-  constexpr int WAIT = PIPE ? LPW + LPW / 2 : PAIR ? LPW : (STAGES - 2) * LPW;  // DMA younger than the k-tile waited for
-  constexpr int RELAX = (PAIR || PIPE) ? 2 : STAGES - 1;                       // waits that an epilogue's stores precede
+  constexpr bool PIPE = CFG::PIPE == 1;
+  constexpr bool PAIR = STAGES == 5 && !PIPE && !PING;
+  constexpr int LEAD = (PAIR || PIPE || PING) ? STAGES - 2 : STAGES - 1;
+  // DMA younger than the k-tile waited for
+  constexpr int WAIT = PING ? 2 * LPW : PIPE ? LPW + LPW / 2 : PAIR ? LPW : (STAGES - 2) * LPW;
+  constexpr int RELAX = (PAIR || PIPE || PING) ? 2 : STAGES - 1;  // waits that an epilogue's stores precede
   constexpr int NST = epilogue_stores<EPI, WTM, SM, SN>();
   constexpr int SLOT = 32 * 64 * 2;  // staging bytes per wave (one 32-row x 64-column pass)
   static_assert(BK == 32 || BK == 64, "swizzles and DMA mapping cover 32- and 64-deep k-tiles");
   constexpr int RB = BK * 2;      // bytes per K-contiguous row of a k-tile
   constexpr int CPR = BK / 8;     // 16-byte chunks per K-contiguous row
   constexpr int RPI = 64 / CPR;   // K-contiguous rows per DMA instruction
-  static_assert(WTM % 32 == 0 && (WTN == 64 || WTN == 128), "wave tiles are whole 32x32 sub-tiles, 64 or 128 columns wide");
+  static_assert(WTM % 32 == 0 && WTN == 64, "wave tiles are whole 32x32 sub-tiles, 64 columns wide");
   static_assert(!PIPE || (STAGES == 5 && LPW % 2 == 0 && BK == 32), "the pipelined loop's stage and DMA schedule");
-  static_assert(NI_A % NWAVES == 0 && NI_B % NWAVES == 0, "DMA instructions of each operand split evenly over waves");
+  // (The weight gradients keep the paired-barrier loop: on ping-pong they
+  // measured 175 against 159 us (C2 down_wgrad) and 1906 against 1864 us
+  // (C5 up_wgrad), the same at C4.)
+  static_assert(!PING || (MODE == MODE_MG && STAGES == 5 && BK == 32 && NWAVES == 8 && WM == 2 && NI_A == NI_B &&
+                          NI_A % 4 == 0),
+                "the ping-pong loop's wave groups, stage and DMA schedule");
+  static_assert(PING || (NI_A % NWAVES == 0 && NI_B % NWAVES == 0), "DMA instructions of each operand split evenly over waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (SN % 2 == 0), "SwiGLU forward pairs gate/up sub-tiles");
   static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
   static_assert(NWAVES * SLOT <= STAGE_BYTES, "the epilogue stages every wave's pass in one ring stage");
@@ -347,7 +359,10 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // Wave-uniform values live in scalar registers: buffer resources and the
   // DMA LDS base (M0) must be uniform.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  // Ping-pong wave groups: group grp = wave / 4 holds wave columns 2 grp and
+  // 2 grp + 1; its four waves sit on the four SIMDs.
+  const int grp = wave >> 2, w4 = wave & 3;
+  const int wm = PING ? (w4 >> 1) : wave / WN, wn = PING ? grp * 2 + (w4 & 1) : wave % WN;
   const int l32 = lane & 31;
   const int khalf = lane >> 5;
 
@@ -482,9 +497,15 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // k-tile, and a per-tile base offset (kOOB if the row or column is outside
   // the tile's valid range).
   const u32x4_t rsA = rsrc_words(p.A, p.a_bytes);
-  // Slot j's instruction: operand and index within the operand's k-tile.
+  // Row strides in bytes, in scalar registers (a ping-pong wave selects its
+  // operand's at run time).
+  const uint32_t lda2 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p.lda) * 2u);
+  const uint32_t ldb2 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p.ldb) * 2u);
+  // Slot j's operand (wave-uniform) and instruction index within the operand's k-tile.
+  auto slot_is_a = [&](int j) { return PING ? grp == 0 : j < LPW_A; };
   auto slot_inst = [&](int j, bool& is_a) {
-    is_a = j < LPW_A;
+    is_a = slot_is_a(j);
+    if constexpr (PING) return w4 * LPW + j;
     return is_a ? wave * LPW_A + j : wave * LPW_B + (j - LPW_A);
   };
   int dma_lds[LPW], dma_k[LPW], dma_col[LPW];
@@ -546,7 +567,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
         if (is_a) {
           const int grow = dt.m0 + r;
           ok = grow < dt.re;
-          row_bytes = static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.lda) * 2u;
+          row_bytes = static_cast<uint32_t>(grow) * lda2;
         } else {
           int wrow;
           if constexpr (EPI == EPI_SWIGLU_FWD) {
@@ -565,12 +586,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
             wrow = dt.n0 + r;
             ok = wrow < p.N;
           }
-          row_bytes = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(p.ldb) * 2u;
+          row_bytes = static_cast<uint32_t>(wrow) * ldb2;
         }
         dma_pre[j2] = ok ? row_bytes + static_cast<uint32_t>(c) * 16u + static_cast<uint32_t>(dt.k_begin) * 2u : kOOB;
       } else {
         const int col = (is_a ? dt.m0 : dt.n0) + dma_col[j2];
-        const uint32_t ld = static_cast<uint32_t>(is_a ? p.lda : p.ldb) * 2u;
+        const uint32_t ld = is_a ? lda2 : ldb2;
         dma_pre[j2] = col < (is_a ? p.M : p.N)
                           ? static_cast<uint32_t>(mc_row0 + dma_k[j2]) * ld + static_cast<uint32_t>(col) * 2u
                           : kOOB;
@@ -591,21 +612,33 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
     const int k_left = dt.kred - k0;  // k (K-contiguous) or k-rows (M/N-contiguous) left in the tile
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      ra[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsA[w]));
-      rb[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsB[w]));
+      if constexpr (PING) {
+        // every slot of a ping-pong wave is of its group's operand
+        ra[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(grp == 0 ? rsA[w] : rsB[w]));
+        rb[w] = ra[w];
+      } else {
+        ra[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsA[w]));
+        rb[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsB[w]));
+      }
     }
     const uint32_t stage_lds = lds_address(ring) + st * STAGE_BYTES;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const bool is_a = j < LPW_A;
-      const uint32_t step = (is_a ? A_KC : B_KC) ? 2u : static_cast<uint32_t>(is_a ? p.lda : p.ldb) * 2u;
+      const bool is_a = slot_is_a(j);
+      const uint32_t step = (is_a ? A_KC : B_KC) ? 2u : (is_a ? lda2 : ldb2);
       // Past the last tile dma_pre is kOOB and stays out of range (the
       // added offset is below the 2 GiB operand limit).
       doff[j] = dma_k[j] < k_left ? dma_pre[j] + static_cast<uint32_t>(k0) * step : kOOB;
       dlds[j] = __builtin_amdgcn_readfirstlane(stage_lds + dma_lds[j]);
     }
   };
-  auto dma_fire = [&](int j) __attribute__((always_inline)) { dma16(j < LPW_A ? ra : rb, doff[j], dlds[j]); };
+  auto dma_fire = [&](int j) __attribute__((always_inline)) {
+    if constexpr (PING) {
+      dma16(ra, doff[j], dlds[j]);
+    } else {
+      dma16(j < LPW_A ? ra : rb, doff[j], dlds[j]);
+    }
+  };
   auto dma_advance = [&]() __attribute__((always_inline)) {
     if (dj < ntiles && ++dk == dt.nk) dma_seek(dj + 1);
   };
@@ -749,16 +782,6 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   const __amdgpu_buffer_rsrc_t rsC2 = make_rsrc(p.C2, p.c2_bytes);  // SwiGLU pre-activation (0 bytes if absent)
 
   auto epilogue = [&](const Tile& t) __attribute__((always_inline)) {
-    if constexpr (PIPE && NWAVES == 4) {
-      // The 256 accumulator registers of a 128x128 wave tile live in AGPRs.
-      // Without this fence the compiler copies every accumulator to a VGPR
-      // right after its last MFMA, in the k-loop, for the conditional
-      // epilogue, which doubles their footprint and spills the k-loop.
-#pragma unroll
-      for (int i = 0; i < SM; ++i)
-#pragma unroll
-        for (int j = 0; j < SN; ++j) asm volatile("" : "+a"(acc[i][j]));
-    }
     const int wcol0 = t.n0 + wn * WTN;
     const int row_limit = (MODE == MODE_MG) ? t.re : p.M;
     // Output resource: MG writes [rows, ldc]; KG one group's [M, ldc]; split-K one split's partial.
@@ -947,7 +970,130 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   for (int s = 0; s < LEAD; ++s) dma_issue(s);
   int cstage = 0, dstage = LEAD;
   int parity = 0;  // k-step count of the stream, mod 2
-  if constexpr (PIPE) {
+  if constexpr (PING) {
+    // Ping-pong.  k-tile c of the block's stream sits in ring stage c % 5.
+    // Group 0 (waves 0-3) reads k-tile c's fragments in phase 2c and
+    // multiplies them in phase 2c + 1; group 1 (waves 4-7) reads them in
+    // phase 2c + 1 and multiplies in phase 2c + 2.  Each phase ends with a
+    // block barrier, so on every SIMD one wave issues MFMAs from registers
+    // while its partner reads fragments and fires DMA.
+    //
+    // DMA: k-tile c's A half is fired by group 0 in phase 2c - 6 and its B
+    // half by group 1 in phase 2c - 5 (the memory phases of k-tile c - 3),
+    // spread among the fragment reads.  Its stage last held k-tile c - 5,
+    // which group 1 read in phase 2c - 9.  Before group 0 reads k-tile c, the
+    // barrier ending phase 2c - 1 follows group 0's wait for its A half (end
+    // of its compute phase 2c - 1: its DMA of phases 2c - 4 and 2c - 2 may be
+    // in flight) and group 1's wait for its B half (end of its memory phase
+    // 2c - 1: its DMA of phases 2c - 3 and 2c - 1 may be in flight).
+    //
+    // A tile ending with k-tile c is written out by group 0 in phase 2c + 2
+    // and by group 1 in phase 2c + 3, each staging through its half of stage
+    // c % 5 (the A half for group 0, the B half for group 1), which the DMA
+    // refills only from phase 2c + 4 (A) and 2c + 5 (B).
+    constexpr int NR = (BK / 16) * (SM + SN);  // fragment reads per memory phase
+    bf16x8_t fa[BK / 16][SM], fb[BK / 16][SN];
+    auto read_frag = [&](const char* stage, int ks, int q) __attribute__((always_inline)) {
+      if (q < SM) {
+        const int i = q;
+        if constexpr (A_KC) {
+          fa[ks][i] = *reinterpret_cast<const bf16x8_t*>(stage + a_kc[ks] + i * WM * 32 * RB);
+        } else {
+          const char* a = stage + a_mc[i] + 16 * ks * BM * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(a + 4 * BM * 2));
+          fa[ks][i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      } else {
+        const int j = q - SM;
+        if constexpr (B_KC) {
+          fb[ks][j] = *reinterpret_cast<const bf16x8_t*>(stage + b_kc[ks] + j * 32 * RB);
+        } else {
+          const char* b = stage + b_mc[j] + 16 * ks * BN * 2;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)b);
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(b + 4 * BN * 2));
+          fb[ks][j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+    };
+    // This wave's half of k-tile 0 landed (its halves of k-tiles 1 and 2 are
+    // younger), then every wave's, via the barrier; group 1 then waits one
+    // phase.
+    wait_vmcnt<WAIT>();
+    barrier();
+    if (grp == 1) barrier();
+    bool pending = false;  // a finished tile waits for its epilogue
+    int pstage = 0;        // ... and stages through this stage's half
+    Tile pt = ct;
+    for (;;) {
+      // ---- memory phase of k-tile c (the stream's k-tile at cstage)
+      if (pending) {
+        pending = false;
+        slot = ring + pstage * STAGE_BYTES + wave * SLOT;
+        epilogue(pt);
+        relax = RELAX;
+        if (!compute_seek(cj + 1)) break;
+      }
+      const char* cur = ring + cstage * STAGE_BYTES;
+      dma_prepare(dstage);
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks)
+#pragma unroll
+        for (int q = 0; q < SM + SN; ++q) {
+          read_frag(cur, ks, q);
+          const int r = ks * (SM + SN) + q;
+#pragma unroll
+          for (int s2 = 0; s2 < LPW; ++s2)
+            if (r == (s2 + 1) * NR / LPW - 1) {
+              __builtin_amdgcn_sched_barrier(0);
+              dma_fire(s2);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+      dma_advance();
+      wait_lgkmcnt0();  // the fragments are in registers before the stage can be refilled
+      const bool drain = relax > 0;
+      if (grp == 1) {
+        if (relax > 0) --relax;
+        if (drain) {
+          wait_vmcnt<WAIT + NST>();
+        } else {
+          wait_vmcnt<WAIT>();
+        }
+      }
+      barrier();
+      // ---- compute phase of k-tile c: row sub-tiles without rows of the
+      // tile skip their MFMAs (wave-uniform branches).
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks)
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+          if (i < n_act) {
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+          }
+      if (grp == 0) {
+        const bool drain0 = relax > 0;
+        if (relax > 0) --relax;
+        if (drain0) {
+          wait_vmcnt<WAIT + NST>();
+        } else {
+          wait_vmcnt<WAIT>();
+        }
+      }
+      barrier();
+      const int done_stage = cstage;
+      dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
+      cstage = cstage + 1 == STAGES ? 0 : cstage + 1;
+      if (++ck == ct.nk) {
+        pending = true;
+        pt = ct;
+        pstage = done_stage;
+      }
+    }
+    if (grp == 0) barrier();
+  } else if constexpr (PIPE) {
     // One wave per SIMD: the matrix pipe is fed only while this wave issues
     // MFMAs, so the fragments of the next half step are read into the other
     // register set while the current half step's MFMAs run, and the block
@@ -1142,6 +1288,11 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
   return launch_status(name);
 }
 
+// Mean rows per expert from which the forward expert GEMMs take the
+// ping-pong loop (C4, 1024: the four row-grouped GEMMs 2769 against 2844 us;
+// C5, 512: 5297 against 5465 us; C2, 256: up_fwd 312 against 305 us).
+constexpr int64_t kPingMinMeanRows = 448;
+
 // Expert GEMM over grouped rows.  256x256 tiles do the most MFMA work per
 // k-step of LDS traffic, but with few output columns their grid (about one
 // or two m-tiles per expert times the column tiles) ends in a poorly
@@ -1157,8 +1308,15 @@ int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   constexpr int64_t kTallMaxMeanRows = 288;
   if (out_cols <= 1024 && static_cast<int64_t>(p.rows) <= kTallMaxMeanRows * p.G)
     return launch<MODE_MG, B_KCONTIG, EPI, TallTile>(p, stream, name);
-  if constexpr (B_KCONTIG) return launch<MODE_MG, B_KCONTIG, EPI, BigTileP>(p, stream, name);
-  return launch<MODE_MG, B_KCONTIG, EPI, BigTile>(p, stream, name);
+  // The ping-pong loop keeps the matrix pipes fed while the partner waves
+  // read fragments and fire the DMA.  It wins for the input gradients (two
+  // transpose reads per weight fragment) at every size, and for the forward
+  // GEMMs once the experts average several m-tiles (their weight tiles then
+  // come from L2); with one or two m-tiles per expert the forward GEMMs
+  // stream every weight k-slice from HBM and time the same on both loops.
+  if (!B_KCONTIG || static_cast<int64_t>(p.rows) >= kPingMinMeanRows * p.G)
+    return launch<MODE_MG, B_KCONTIG, EPI, PingTile>(p, stream, name);
+  return launch<MODE_MG, B_KCONTIG, EPI, BigTileP>(p, stream, name);
 }
 
 // Operand checks.  `a` holds M rows, as does `b` when b_rows (the weight

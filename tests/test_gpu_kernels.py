@@ -251,6 +251,10 @@ GEMM_CASES = [
     ("single", [1000], 128, 256),
     ("split", [770, 257, 33], 1280, 64),  # m-tiles of 224/224/224/98 and 160/97 rows
     ("skewed", [0, 0, 3000, 0, 1, 0, 0, 0], 1536, 128),  # one group of 12 m-tiles, the rest empty or one row
+    # at least 448 rows per expert on average: the row-grouped GEMMs take the ping-pong loop
+    ("ping", [900, 0, 1100, 17, 513, 2000], 1536, 2048),
+    ("ping_ragged", [1700, 3, 0, 640, 70], 200, 72),  # ragged n-tile, K tail inside the third k-tile
+    ("ping_shortk", [520, 480, 33], 264, 40),  # two k-tiles (one nearly empty) per tile
 ]
 
 
@@ -314,7 +318,8 @@ def test_grouped_gemm_wgrad(name, cnt, N, K, accumulate, f32):
             close_bf16(dw[e], ref, f"wgrad {name} g{e}", max_rel=8e-3)
 
 
-@pytest.mark.parametrize("cnt,I,H", [([256, 0, 300, 1, 128], 768, 2048), ([5, 64, 0, 17], 64, 96)])
+@pytest.mark.parametrize("cnt,I,H", [([256, 0, 300, 1, 128], 768, 2048), ([5, 64, 0, 17], 64, 96),
+                                     ([600, 0, 1500, 5, 257], 768, 2048)])  # the last on the ping-pong loop
 def test_swiglu_fwd_and_fused_backward(cnt, I, H):
     counts, offs = _groups(cnt)
     M = int(counts.sum())
