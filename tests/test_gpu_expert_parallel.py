@@ -16,6 +16,7 @@ from parallel_amd import (
     ReplicatedTokenExpertParallel,
     SequenceParallelExpertParallel,
     SparseMoeBlock,
+    TokenDispatcher,
     ops,
     verify_expert_modules,
 )
@@ -53,10 +54,10 @@ def ep_model(w, inp, ep, rank, layers=2):
     return model.to(DEV, BF), part
 
 
-def run_share(runtime_cls, w, inp, ep, rank):
+def run_share(runtime_cls, w, inp, ep, rank, layers=2):
     """Forward + backward of <block(x), d_out> through the first layer of the
     model with ``runtime_cls`` installed for (ep, rank)."""
-    model, part = ep_model(w, inp, ep, rank)
+    model, part = ep_model(w, inp, ep, rank, layers)
     verify_expert_modules(model, part)
     rt = runtime_cls(part, None)
     rt.apply(model)
@@ -135,3 +136,73 @@ def test_dispatch_send_buffer_bit_exact(T, E, local, seed, k, H):
     assert tuple(counts.cpu().tolist()) == rsplits
     # pos_of_slot is the inverse of the send order
     assert torch.equal(src.cpu()[pos.cpu().long()], torch.arange(T).repeat_interleave(k))
+
+
+def test_sp_runtime_c2_layer_ep2_shares_sum_to_the_block():
+    """The dispatch runtime on the C2 layer (H 2048, 128 experts, top-8, I 768,
+    4096 tokens) at ep = 2, each rank's share in turn (64 local experts, about
+    16k routed rows each): the shares' outputs, input gradients and router
+    gradients sum to the unsharded block's (ep = 1, same runtime); the block
+    and each share equal the oracle's experts on 48 sampled tokens, on the
+    block's own routes localized to the share
+    (expert_parallel.py:124-231; the reference's tests/test_model_parallel.py:309-339)."""
+    w = WORKLOADS["c2"]
+    inp = make_block_inputs(w, seed=41, device=DEV, dtype=BF, weights_on_device_rng=True)
+    full = run_share(SequenceParallelExpertParallel, w, inp, 1, 0, layers=1)
+    shares = [run_share(SequenceParallelExpertParallel, w, inp, 2, r, layers=1) for r in range(2)]
+    for i, name in enumerate(("out", "dx", "d_router")):
+        close_bf16(shares[0][i].float() + shares[1][i].float(), full[i], f"c2 ep2 sum of {name}")
+    x = inp["x"]
+    _, scores, idx = ops.router_fwd(x, inp["router_weight"], w.top_k, w.norm_topk_prob)
+    sample = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(5))[:48]
+    xs, ids, scs = x.cpu()[sample], idx.cpu()[sample], scores.cpu()[sample]
+    gu, dn = inp["gate_up_proj"].cpu(), inp["down_proj"].cpu()
+    close_bf16(full[0].cpu()[sample], O.experts_grouped(xs, ids, scs, gu, dn), "c2 block, sampled tokens")
+    for rank in range(2):
+        part = ExpertPartition(w.experts, 2, rank)
+        li, ls, _ = part.localize_routes(ids, scs)
+        want = O.experts_grouped(xs, li, ls, gu[part.start:part.stop], dn[part.start:part.stop])
+        close_bf16(shares[rank][0].cpu()[sample], want, f"c2 rank {rank} share, sampled tokens")
+
+
+@pytest.mark.parametrize("rank", [0, 1])
+def test_zero_receive_dispatch_through_the_experts(rank):
+    """The reference's zero-receive case (its tests/test_sequence_parallel.py:17-73)
+    on the kernels: ep = 2 and every route owned by rank 0.  Rank 1's share
+    receives no rows; dispatch, the experts on the empty receive buffer and
+    the combine run without a launch error and give zero output, zero input
+    and score gradients and zero weight gradients.  Rank 0's share receives
+    every route and equals the oracle's experts, backward included."""
+    T, H, k, E, I = 96, 64, 2, 4, 32
+    g = torch.Generator().manual_seed(31)
+    part = ExpertPartition(E, 2, rank)
+    x = torch.randn(T, H, generator=g).to(BF)
+    raw = torch.rand(T, k, generator=g) + 0.1
+    sc = raw / raw.sum(1, keepdim=True)
+    indices = torch.stack([torch.randperm(E // 2, generator=g)[:k] for _ in range(T)])  # all on rank 0
+    gu_all = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(BF)
+    dn_all = (torch.randn(E, H, I, generator=g) * 0.05).to(BF)
+    hidden = x.to(DEV).requires_grad_()
+    scores = sc.to(DEV).requires_grad_()
+    gu = gu_all[part.start:part.stop].to(DEV).requires_grad_()
+    dn = dn_all[part.start:part.stop].to(DEV).requires_grad_()
+    dispatcher = TokenDispatcher(part, None)
+    received, local_idx, received_scores, state = dispatcher.dispatch(hidden, indices.to(DEV), scores)
+    assert local_idx.shape == (T * k if rank == 0 else 0, 1)
+    assert state.send_splits == (T * k, 0) and state.receive_splits == ((T * k, 0) if rank == 0 else (0, 0))
+    y = ops.experts(received, local_idx, received_scores, gu, dn)
+    combined = dispatcher.combine(y, state)
+    combined.float().square().sum().backward()
+    torch.cuda.synchronize()
+    if rank == 1:
+        assert received.shape == (0, H) and y.shape == (0, H)
+        assert not combined.any(), "a share that receives nothing returns zeros"
+        for name, t in (("hidden", hidden), ("scores", scores), ("gate_up_proj", gu), ("down_proj", dn)):
+            assert t.grad is not None and not t.grad.any(), f"{name}: gradient of an empty share must be zero"
+        return
+    leaves = [t.clone().float().requires_grad_() for t in (x, sc, gu_all[:E // 2], dn_all[:E // 2])]
+    ref = O.experts_grouped(leaves[0], indices, leaves[1], leaves[2], leaves[3])
+    ref.square().sum().backward()
+    close_bf16(combined, ref, "rank 0 combined")
+    for name, a, b in zip(("hidden", "scores", "gate_up_proj", "down_proj"), (hidden, scores, gu, dn), leaves):
+        close_bf16(a.grad, b.grad, f"rank 0 d_{name}")

@@ -15,13 +15,15 @@ in seconds):
   the oracle's top-k on the returned logits, bit for bit.
 """
 
+from dataclasses import replace
+
 import pytest
 import torch
 
 from conftest import close_bf16, routing_check
 from oracle import moe_oracle as O
 from parallel_amd import _lib, ops
-from parallel_amd.workloads import WORKLOADS, make_block_inputs
+from parallel_amd.workloads import WORKLOADS, ep_receive_buffer, make_block_inputs
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -175,3 +177,26 @@ def test_full_c4_gradient_accumulation_fused_equals_torch_add():
         grads[fused] = (gu.grad, dn.grad)
     for a, b, label in zip(grads[True], grads[False], ("d_gate_up", "d_down")):
         assert torch.equal(a, b), f"fused {label} accumulation differs from torch's add"
+
+
+def test_full_c3_receive_buffer_every_expert():
+    """C3 at its stated size: rank 0's receive buffer of an EP = 2 group,
+    2 x 4096 source tokens x 8 slots drawn Zipf(1.2) over 128 experts (about
+    24k rows, source-rank-major, expert-contiguous within a source, at least
+    4 of the 64 local experts empty), through the experts forward and
+    backward, with every expert's products checked as above
+    (token_dispatch.py:101-158)."""
+    w3 = WORKLOADS["c3"]
+    _, _, (src, tok, lexp, lsc) = ep_receive_buffer(w3, seed=3)
+    R = int(src.shape[0])
+    inp = make_block_inputs(w3, seed=3, device=DEV, dtype=BF, weights_on_device_rng=True)
+    xs = torch.randn(w3.sources, w3.tokens, w3.hidden, generator=torch.Generator(device=DEV).manual_seed(8),
+                     device=DEV).to(BF)
+    hidden = xs[torch.from_numpy(src).to(DEV), torch.from_numpy(tok).to(DEV)].contiguous()
+    idx = torch.from_numpy(lexp).to(DEV).view(R, 1)
+    sc = torch.from_numpy(lsc).to(DEV).view(R, 1)
+    saved = ops.experts_fwd(hidden, idx, sc, inp["gate_up_proj"], inp["down_proj"])
+    recv = replace(w3, name="c3_receive", batch=1, seq=R, top_k=1, experts=w3.local_experts, local_experts=None)
+    counts = _backward_checks("c3", recv, inp, sc, saved, 62)
+    assert sum(c == 0 for c in counts) >= 4, "some local experts must be empty"
+    assert max(counts) > 4 * R // len(counts), "Zipf routing must be skewed"
