@@ -108,6 +108,19 @@ int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices,
                              int norm_topk_prob, void* d_logits_bf16,
                              void* stream);
 
+/* Backward of the router top-k for bf16 router logits (the reference's
+ * F.linear under bf16 autocast, parallel/parallel/engine/engine.py:141,
+ * TF/models/qwen3_moe/modeling_qwen3_moe.py:260-265): logits[T,E] holds the
+ * f32 values of the bf16 logits and d_logits (may be NULL) the values of
+ * their incoming bf16 gradient [T,E] as f32.  As autograd sums a bf16
+ * tensor's gradients in bf16, d_logits_bf16 = bf16(bf16(g) + d_logits), g
+ * being the f32 softmax / top-k / renorm backward. */
+int moe_router_bf16_logits_bwd(const float* logits, const int64_t* indices,
+                               const float* d_scores, const float* d_logits,
+                               int64_t T, int64_t E, int64_t k,
+                               int norm_topk_prob, void* d_logits_bf16,
+                               void* stream);
+
 /* moe_router_topk_bwd_bf16 with the aux loss's logits gradient (that of
  * moe_aux_loss_bwd for token_weight, stats and d_aux[1], which are what
  * moe_router_aux_fwd returned and the loss's incoming gradient) computed in
@@ -195,8 +208,9 @@ int moe_router_aux_fwd(const void* x, const void* wr, const float* logit_bias,
 /* ----------------------------------------------------------------- permute */
 
 /* Stable counting sort of S = T*k routed slots by bucket = ids[s] / divisor
- * (floor division; ids >= 0).  Slots whose bucket is >= num_buckets are
- * sentinels: they sort after every real bucket and are excluded from counts.
+ * (floor division).  Slots whose id is negative or whose bucket is >=
+ * num_buckets are sentinels: they sort after every real bucket and are
+ * excluded from counts.
  * Outputs (int32):
  *   perm[S]        sorted position -> slot index s = t*k + j
  *   pos_of_slot[S] slot index -> sorted position (inverse of perm)
@@ -227,6 +241,9 @@ int moe_permute_fwd(const void* hidden, int64_t T, int64_t H,
  * before any launch.  Calls no hipMalloc or other allocating routine.  Every
  * call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams, threads or graph replays in flight together) race.
+ * Make the first call on each device outside graph capture: it looks up the
+ * array's device address (hipGetSymbolAddress), which may load the library's
+ * code onto that device.  Later calls may be captured and replayed.
  * Outputs and semantics are those of moe_permute_fwd, bit for bit. */
 int moe_permute_fwd_noalloc(const void* hidden, int64_t T, int64_t H,
                             const int64_t* ids, int64_t k, int64_t divisor,

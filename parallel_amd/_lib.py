@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
 # MOE_MI355X_LIB selects another build of the same library (A/B comparisons).
 LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB") or Path(__file__).resolve().parent / "lib" / "libmoe_mi355x.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MOE_OK = 0
 MOE_ERR_INVALID = -1
@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_router_topk_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "moe_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _I, _P, _P]),
     "moe_router_topk_bwd_bf16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
+    "moe_router_bf16_logits_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "moe_router_aux_bwd_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "moe_aux_loss_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_aux_loss_fwd": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),

@@ -551,11 +551,19 @@ __global__ void reduce_partials_bf16_kernel(const float* __restrict__ partials, 
 // aux_bwd_kernel computes it (from the same softmax) and added where d_add
 // would be: the result is the bits of aux_bwd_kernel's output passed as
 // d_add.
+//
+// With bf16_terms (the bf16-logit router) the logits are a bf16 tensor in the
+// reference (the router linear under bf16 autocast), and autograd sums the
+// gradients its consumers return, each already bf16, in bf16: the softmax
+// path's gradient and the aux term are rounded to bf16 first and every sum
+// is rounded again, as bf16(bf16(softmax path) + bf16(bf16(aux) + d_add)),
+// d_add holding a bf16 gradient's values.
 template <int LPT, int NPL, int KT>
 __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ indices, const float* __restrict__ d_scores, int T,
     int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16,
-    const float* __restrict__ token_weight, const float* __restrict__ aux_stats, const float* __restrict__ d_aux) {
+    const float* __restrict__ token_weight, const float* __restrict__ aux_stats, const float* __restrict__ d_aux,
+    int bf16_terms) {
   constexpr int KM = KT ? KT : kMaxTopK;
   const int k = KT ? KT : k_rt;
   const int sub = Tok<LPT>::sub();
@@ -574,6 +582,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
   }
   const SoftmaxStats st = softmax_stats<LPT>(v);
   const float inv_sum = 1.0f / st.sum;
+  auto round_bf16 = [](float x) { return bf16_to_f32(f32_to_bf16(x)); };
   if (aux_stats) {
     // aux_bwd_kernel's term: p_e (g_e - <g, p>), g_e = d_aux E w c_e / W^2.
     const float W = aux_stats[E];
@@ -596,7 +605,11 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const float d = p[j] * (g[j] - dot);
-      add[j] = d_add ? add[j] + d : d;
+      if (bf16_terms) {
+        add[j] = d_add ? round_bf16(add[j] + round_bf16(d)) : round_bf16(d);
+      } else {
+        add[j] = d_add ? add[j] + d : d;
+      }
     }
   }
 
@@ -656,6 +669,7 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
         if (r < k && idx[r] == e) dp += dv[r];
       float p = expf(v[j] - st.max) * inv_sum;
       float g = p * (dp - c);
+      if (bf16_terms) g = round_bf16(g);
       if (d_add || aux_stats) g += add[j];
       if (d_logits) d_logits[base + e] = g;
       if (d_logits_bf16) d_logits_bf16[base + e] = f32_to_bf16(g);
@@ -921,27 +935,43 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
                        accumulate ? d_logits : nullptr, d_logits, static_cast<bf16_t*>(d_logits_bf16), nullptr,
-                       nullptr, nullptr);
+                       nullptr, nullptr, 0);
   });
   return launch_status("moe_router_topk_bwd");
 }
 
-extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
-                                        const float* d_add, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
-                                        void* d_logits_bf16, void* stream) {
+namespace {
+int topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores, const float* d_add, int64_t T,
+                  int64_t E, int64_t k, int norm_topk_prob, void* d_logits_bf16, int bf16_terms, void* stream,
+                  const char* name) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
-  MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "router topk bwd bf16: null pointer");
+  MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "%s: null pointer", name);
   int blocks = token_blocks(T, E, true);
   with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
                        dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), nullptr, nullptr, nullptr);
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), nullptr, nullptr, nullptr, bf16_terms);
   });
-  return launch_status("moe_router_topk_bwd_bf16");
+  return launch_status(name);
+}
+}  // namespace
+
+extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
+                                        const float* d_add, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                                        void* d_logits_bf16, void* stream) {
+  return topk_bwd_bf16(logits, indices, d_scores, d_add, T, E, k, norm_topk_prob, d_logits_bf16, 0, stream,
+                       "moe_router_topk_bwd_bf16");
+}
+
+extern "C" int moe_router_bf16_logits_bwd(const float* logits, const int64_t* indices, const float* d_scores,
+                                          const float* d_logits, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                                          void* d_logits_bf16, void* stream) {
+  return topk_bwd_bf16(logits, indices, d_scores, d_logits, T, E, k, norm_topk_prob, d_logits_bf16, 1, stream,
+                       "moe_router_bf16_logits_bwd");
 }
 
 extern "C" int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
@@ -959,7 +989,7 @@ extern "C" int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indic
                        dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), token_weight, stats, d_aux);
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), token_weight, stats, d_aux, 0);
   });
   return launch_status("moe_router_aux_bwd_bf16");
 }

@@ -179,14 +179,17 @@ def _router_bwd_f32(x, weight, logits, indices, d_logits, d_scores, norm_topk_pr
 def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tensor, d_logits: Tensor | None,
                        d_scores: Tensor | None, norm_topk_prob: bool, token_weight: Tensor | None = None,
                        stats: Tensor | None = None, d_aux: Tensor | None = None,
-                       dw_target: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
+                       dw_target: Tensor | None = None, bf16_logits: bool = False) -> tuple[Tensor, Tensor | None]:
     """The router backward's launches: (dx [T,H] bf16, dweight [E,H] bf16).
 
     d_logits is the logits' incoming gradient (fp32, may be None); with
     ``d_aux`` (and the ``stats``/``token_weight`` of router_aux_fwd) the aux
     loss's logits gradient is added in the same top-k backward pass.  With
     ``dw_target`` (the router weight's existing bf16 gradient) the weight
-    gradient is added into it and None is returned in its place.  fp32
+    gradient is added into it and None is returned in its place.  With
+    ``bf16_logits`` the logits were bf16 (router_fwd_bf16) and d_logits is
+    their bf16 gradient: the softmax path's gradient is rounded to bf16
+    before it is added, as autograd adds a bf16 tensor's gradients.  fp32
     modules get fp32 gradients from the fp32 kernels."""
     if x.dtype == weight.dtype == torch.float32:
         return _router_bwd_f32(x.contiguous(), weight.contiguous(), logits, indices, d_logits, d_scores,
@@ -204,7 +207,12 @@ def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tenso
     d_scores = d_scores.float().contiguous()
     # Only the bf16 d_logits feeds the GEMMs; the incoming logits gradient is
     # read, not copied.
-    if d_aux is not None:
+    if bf16_logits:
+        if d_aux is not None:
+            raise ValueError("the bf16-logit router's backward takes the aux loss's gradient as d_logits")
+        call("moe_router_bf16_logits_bwd", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
+             int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
+    elif d_aux is not None:
         tw = None if token_weight is None else token_weight.float().contiguous()
         da = d_aux.float().reshape(1).contiguous()
         call("moe_router_aux_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), ptr(tw), ptr(stats),
@@ -298,7 +306,7 @@ def _router_bf16_backward(ctx, d_logits, d_scores, _d_idx, _d_logits32):
     x, weight, logits, idx = ctx.saved_tensors
     dl = None if d_logits is None else d_logits.float()
     ds = None if d_scores is None else d_scores.float()
-    dx, dw = router_bwd_kernels(x, weight, logits, idx, dl, ds, ctx.norm)
+    dx, dw = router_bwd_kernels(x, weight, logits, idx, dl, ds, ctx.norm, bf16_logits=True)
     return dx, dw, None, None, None
 
 
@@ -840,8 +848,21 @@ def experts(hidden: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_
     the result is the same bits.  Autograd sees no gradient for such a weight,
     so its post-accumulate-grad hooks do not run: leave it off where an FSDP
     unit waits for those hooks (parallel/parallel/engine/_dp_param_unit.py:669-690).
-    A weight without a ``.grad`` gets a fresh gradient as usual."""
+    A weight without a ``.grad`` gets a fresh gradient as usual.
+
+    The in-place write is invisible to autograd and to tracing: tensor grad
+    hooks and post-accumulate-grad hooks of such a weight do not run, and
+    under ``torch.compile`` (AOTAutograd) the option is refused."""
+    _refuse_traced_accumulation(accumulate_grad, "experts")
     return experts_fwd(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_grad)[0]
+
+
+def _refuse_traced_accumulation(accumulate_grad: bool, what: str) -> None:
+    """accumulate_grad writes param.grad from inside a custom op's backward,
+    a side effect that torch.compile / AOTAutograd cannot trace."""
+    if accumulate_grad and torch.compiler.is_compiling():
+        raise RuntimeError(f"{what}(accumulate_grad=True) adds into .grad inside the backward, which torch.compile "
+                           "cannot trace; use accumulate_grad=False under torch.compile")
 
 
 # --------------------------------------------- the whole block in one op
@@ -948,7 +969,9 @@ def moe_block(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj:
     the aux loss's logits gradient inside the top-k backward, and with
     ``accumulate_grad`` adds every weight gradient into an existing ``.grad``
     (bf16 router weight; bf16 or fp32 expert weights) in the kernels, as
-    ``experts`` does for the expert weights."""
+    ``experts`` does for the expert weights (with the same limits: no grad
+    hooks for those weights, refused under ``torch.compile``)."""
+    _refuse_traced_accumulation(accumulate_grad, "moe_block")
     out, logits, scores, idx, aux = moe_block_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
                                                   token_weight, logit_bias, accumulate_grad)[:5]
     return out, logits, scores, idx, aux

@@ -231,3 +231,52 @@ def test_bf16_logit_router_backward_and_the_autocast_module():
         lm, sm, im = router(x.to(DEV))
     assert lm.dtype == BF and sm.dtype == BF
     assert torch.equal(lm, logits_b.detach()) and torch.equal(im, idx) and torch.equal(sm, scores.detach())
+
+
+def test_bf16_logit_router_backward_sums_its_logit_gradients_in_bf16():
+    """Under bf16 autocast the reference's router logits are a bf16 tensor read
+    by two consumers, the router's fp32 softmax and the aux loss
+    (load_balancing_loss_func, TF modeling_qwen3_moe.py:514-593); autograd
+    returns each consumer's gradient in bf16 and adds them in bf16.
+    moe_router_bf16_logits_bwd with the aux loss's bf16 gradient as d_logits gives
+    the bits of CPU autograd on the bf16 logits (up to the rare bf16 rounding
+    flip of a one-ulp fp32 difference in the softmax path); rounding the fp32
+    sum once instead differs on more than 1 % of the logits here.  Without
+    renormalisation, so that every logit's softmax-path gradient is well
+    conditioned (renormalised top-k makes the unselected logits' gradient
+    exactly zero in exact arithmetic, and what either side computes there is
+    rounding noise)."""
+    from parallel_amd import _lib
+
+    T, H, E, k, coef = 512, 256, 64, 6, 1.0
+    x = torch.randn(T, H, generator=gen(41)).to(BF)
+    w = (torch.randn(E, H, generator=gen(42)) * 0.05).to(BF)
+    d_scores = torch.randn(T, k, generator=gen(43)).to(BF)
+    logits_b, _, idx, logits32 = ops.router_fwd_bf16(x.to(DEV), w.to(DEV), k, False)
+    ic = idx.cpu()
+
+    def softmax_path(lg):
+        top = torch.softmax(lg.float(), dim=-1).gather(1, ic)
+        return (top.to(BF).float() * d_scores.float()).sum()
+
+    lb = logits_b.cpu().requires_grad_()
+    (softmax_path(lb) + coef * O.load_balancing_loss(lb.float(), E, k)).backward()
+    la = logits_b.cpu().requires_grad_()
+    (coef * O.load_balancing_loss(la.float(), E, k)).backward()
+    d_add = la.grad.float()
+    got = torch.empty(T, E, dtype=BF, device=DEV)
+    _lib.call("moe_router_bf16_logits_bwd", logits32.data_ptr(), idx.data_ptr(), (ds := d_scores.float().to(DEV)).data_ptr(),
+              (da := d_add.to(DEV)).data_ptr(), T, E, k, 0, got.data_ptr(), _lib.stream_of(got))
+    torch.cuda.synchronize()
+    got, want = got.cpu(), lb.grad
+    lf = logits_b.cpu().float().requires_grad_()
+    softmax_path(lf).backward()
+    # A rounding flip of the softmax path's term moves the sum by one bf16
+    # step of the larger term (more than one step of the sum where the two
+    # terms cancel).
+    term = torch.maximum(lf.grad.abs(), d_add.abs())
+    ulp = torch.ldexp(torch.ones(T, E), torch.frexp(term)[1] - 8)
+    assert ((got.float() - want.float()).abs() <= ulp).all(), "more than one bf16 step of a term from the reference"
+    assert (got == want).float().mean() >= 0.999
+    once = (lf.grad + d_add).to(BF)
+    assert (once != want).float().mean() > 0.01, "the test data must separate one rounding from two"

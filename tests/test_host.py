@@ -191,3 +191,21 @@ def test_zero_size_calls_accept_null_buffers_without_a_gpu():
     # a missing non-empty operand is still an error
     assert lib.moe_grouped_gemm_fwd(None, None, b, E, 0, H, I, None, None) == _lib.MOE_ERR_INVALID
     assert lib.moe_grouped_gemm_fwd(None, b, b, E, 8, H, I, None, None) == _lib.MOE_ERR_INVALID
+
+
+def test_accumulate_grad_is_refused_under_torch_compile(monkeypatch):
+    """accumulate_grad writes .grad from inside the backward, which tracing
+    cannot see: the ops refuse it while torch.compile traces them (checked
+    before any tensor reaches the library)."""
+    import torch
+
+    from parallel_amd import ops
+
+    monkeypatch.setattr(torch.compiler, "is_compiling", lambda: True)
+    x = torch.zeros(4, 8)
+    with pytest.raises(RuntimeError, match="torch.compile"):
+        ops.experts(x, torch.zeros(4, 2, dtype=torch.int64), torch.zeros(4, 2), torch.zeros(2, 8, 8),
+                    torch.zeros(2, 8, 4), accumulate_grad=True)
+    with pytest.raises(RuntimeError, match="torch.compile"):
+        ops.moe_block(x, torch.zeros(2, 8), torch.zeros(2, 8, 8), torch.zeros(2, 8, 4), 2, True,
+                      accumulate_grad=True)

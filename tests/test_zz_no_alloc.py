@@ -1,7 +1,8 @@
 """The allocation-free routing permutation (moe_permute_fwd_noalloc) against
 moe_permute_fwd, through the C ABI: bit-identical outputs on two calls in a
 row, the second smaller (its fixed scratch keeps the first call's contents),
-and the size limit refused before any launch."""
+replays of a captured HIP graph, no device allocation by a call, and the size
+limit refused before any launch."""
 
 import ctypes
 
@@ -81,6 +82,47 @@ def test_noalloc_permute_at_its_largest_size():
     for label, a, b in zip(("perm", "pos_of_slot", "counts", "offsets"), outs["moe_permute_fwd_noalloc"],
                            outs["moe_permute_fwd"]):
         assert torch.equal(a, b), label
+
+
+@pytest.mark.gpu
+def test_noalloc_permute_in_a_captured_graph():
+    """After one eager call on the device (which resolves the scratch array's
+    address), a second eager call leaves the device's free memory unchanged;
+    a call captured into a HIP graph and replayed three times, on new ids
+    written in place before each replay and with the workspace entry point
+    run eagerly between replays, equals moe_permute_fwd on the same ids bit
+    for bit every time."""
+    T, k, divisor, nb, H = 2048, 8, 1, 128, 256
+    g = torch.Generator().manual_seed(5)
+    hidden = torch.randn(T, H, generator=g).to(BF).to(DEV)
+    ids = torch.randint(-1, nb + 1, (T, k), generator=g).to(DEV)
+    lib = _lib.load()
+    outs = _outputs(T, k, nb, H, DEV)
+
+    def call(stream):
+        _lib.check(lib.moe_permute_fwd_noalloc(hidden.data_ptr(), T, H, ids.data_ptr(), k, divisor, nb,
+                                               *(o.data_ptr() for o in outs), stream), "moe_permute_fwd_noalloc")
+
+    call(_lib.stream_of(hidden))
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    call(_lib.stream_of(hidden))
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free_before, "an eager call changed the device's free memory"
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        ids.copy_(torch.randint(-1, nb + 1, (T, k), generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _run("moe_permute_fwd", hidden, ids, divisor, nb)
+        torch.cuda.synchronize()
+        n = int(want[4][-1])
+        for label, a, b in zip(("rows", "perm", "pos_of_slot", "counts", "offsets"), outs, want):
+            if label == "rows":
+                a, b = a[:n], b[:n]
+            assert torch.equal(a, b), f"replay {rep}: {label}"
 
 
 def test_noalloc_permute_refuses_sizes_beyond_its_scratch():
