@@ -420,7 +420,7 @@ def calibration(w) -> dict:
     return out
 
 
-def measure(w, steps: int, warmup: int, instrumented_steps: int, event_every: int = 4):
+def measure(w, steps: int, warmup: int, instrumented_steps: int, event_every: int = 4, bf16_logits: bool = False):
     """Builds workload w's inputs on the GPU, runs `warmup` steps, an
     instrumented pass (events around every launch, outside the timed region)
     and `steps` timed steps in which only the dominant entry point carries
@@ -491,7 +491,8 @@ def measure(w, steps: int, warmup: int, instrumented_steps: int, event_every: in
             # recomputes both from the logits), and the backward adds the
             # router's input gradient to the experts' inside the permute
             # backward instead of a separate elementwise add.
-            out, _, _, _, aux = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob, None, bias, accumulate)
+            out, _, _, _, aux = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob, None, bias, accumulate,
+                                              bf16_logits)
             torch.autograd.backward([out, aux], [d_out, coef])
 
     for _ in range(args.warmup):
@@ -542,6 +543,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2",
                     help="workload key (c1 c2 c3 c4 c5); c2 is the headline, c1 the reference's fp32 CPU case")
+    ap.add_argument("--router-logits", choices=("fp32", "bf16"), default="fp32",
+                    help="router logits dtype: fp32 (the configurations' statement) or bf16 (the reference's "
+                         "router under bf16 autocast)")
     ap.add_argument("--event-every", type=int, default=4,
                     help="timed steps per step whose dominant-kernel launches carry HIP events")
     ap.add_argument("--instrumented-steps", type=int, default=3,
@@ -596,7 +600,8 @@ def main() -> int:
     from parallel_amd.workloads import WORKLOADS, make_block_inputs
 
     w = WORKLOADS[args.config]
-    m = measure(w, args.steps, args.warmup, args.instrumented_steps, max(1, args.event_every))
+    m = measure(w, args.steps, args.warmup, args.instrumented_steps, max(1, args.event_every),
+                args.router_logits == "bf16")
     ms_per_step, tokens_per_s, elapsed = m["ms_per_step"], m["tokens_per_s"], m["elapsed"]
     durations, dominant, dominant_ms, rows = m["durations"], m["dominant"], m["dominant_ms"], m["rows"]
 
@@ -698,7 +703,7 @@ def main() -> int:
         "config": {"workload": {"c1": "c1: tiny Qwen3-MoE block (fp32)", "c2": "c2: Qwen3-30B-A3B MoE block",
                                 "c4": "c4: Qwen3-30B-A3B MoE block"}.get(w.name, w.name),
                    "tokens": w.tokens, "hidden": w.hidden, "experts": w.experts, "top_k": w.top_k,
-                   "moe_intermediate": w.intermediate, "router_logits": "fp32", "aux_coef": w.aux_coef,
+                   "moe_intermediate": w.intermediate, "router_logits": args.router_logits, "aux_coef": w.aux_coef,
                    "dW": "accumulated into existing gradients" if w.name == "c4" else "written"},
         "grouped_gemm": {"flops_fwd_bwd": gemm_flops, "time_ms": round(gemm_s * 1e3, 4),
                          "tflops": round(gemm_tflops, 1) if gemm_tflops else None,

@@ -112,14 +112,20 @@ int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices,
  * F.linear under bf16 autocast, parallel/parallel/engine/engine.py:141,
  * TF/models/qwen3_moe/modeling_qwen3_moe.py:260-265): logits[T,E] holds the
  * f32 values of the bf16 logits and d_logits (may be NULL) the values of
- * their incoming bf16 gradient [T,E] as f32.  As autograd sums a bf16
- * tensor's gradients in bf16, d_logits_bf16 = bf16(bf16(g) + d_logits), g
- * being the f32 softmax / top-k / renorm backward. */
+ * their incoming bf16 gradient [T,E] as f32.  With stats and d_aux (both or
+ * neither; token_weight may be NULL) the aux loss's logits gradient of
+ * moe_aux_loss_bwd over those logits is formed in the same pass (the aux loss
+ * of load_balancing_loss_func, :514-593, on the bf16 logits).  As autograd
+ * sums a bf16 tensor's gradients in bf16, each term is rounded to bf16 and
+ * every sum again: d_logits_bf16 = bf16(bf16(g) + bf16(bf16(aux) + d_logits)),
+ * g being the f32 softmax / top-k / renorm backward of d_scores rounded to
+ * bf16 (the scores of bf16 logits are bf16, :266, and so is their gradient). */
 int moe_router_bf16_logits_bwd(const float* logits, const int64_t* indices,
                                const float* d_scores, const float* d_logits,
-                               int64_t T, int64_t E, int64_t k,
-                               int norm_topk_prob, void* d_logits_bf16,
-                               void* stream);
+                               const float* token_weight, const float* stats,
+                               const float* d_aux, int64_t T, int64_t E,
+                               int64_t k, int norm_topk_prob,
+                               void* d_logits_bf16, void* stream);
 
 /* moe_router_topk_bwd_bf16 with the aux loss's logits gradient (that of
  * moe_aux_loss_bwd for token_weight, stats and d_aux[1], which are what

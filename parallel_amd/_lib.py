@@ -43,7 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_router_topk_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "moe_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _I, _P, _P]),
     "moe_router_topk_bwd_bf16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
-    "moe_router_bf16_logits_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
+    "moe_router_bf16_logits_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "moe_router_aux_bwd_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "moe_aux_loss_workspace_bytes": (_SZ, [_I64, _I64]),
     "moe_aux_loss_fwd": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),

@@ -623,6 +623,8 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
       bool ok = id >= 0 && id < E;
       idx[r] = ok ? static_cast<int>(id) : -1;
       ds[r] = d_scores[static_cast<int64_t>(t) * k + r];
+      // bf16 logits come with bf16 scores, whose gradient is a bf16 tensor
+      if (bf16_terms) ds[r] = round_bf16(ds[r]);
       float lv;
       if constexpr (LPT == kWave) {
         // One token per wave: the selected logit is already in lane e % 64
@@ -941,20 +943,21 @@ extern "C" int moe_router_topk_bwd(const float* logits, const int64_t* indices, 
 }
 
 namespace {
-int topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores, const float* d_add, int64_t T,
-                  int64_t E, int64_t k, int norm_topk_prob, void* d_logits_bf16, int bf16_terms, void* stream,
-                  const char* name) {
+int topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores, const float* d_add,
+                  const float* token_weight, const float* stats, const float* d_aux, int64_t T, int64_t E, int64_t k,
+                  int norm_topk_prob, void* d_logits_bf16, int bf16_terms, void* stream, const char* name) {
   int rc = check_router(T, E, k);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
   MOE_REQUIRE(logits && indices && d_scores && d_logits_bf16, MOE_ERR_INVALID, "%s: null pointer", name);
+  MOE_REQUIRE(!stats == !d_aux, MOE_ERR_INVALID, "%s: stats and d_aux go together", name);
   int blocks = token_blocks(T, E, true);
   with_npl_k<true>(E, k, [&](auto L, auto N, auto K) {
     hipLaunchKernelGGL((router_topk_bwd_kernel<decltype(L)::value, decltype(N)::value, decltype(K)::value>),
                        dim3(blocks),
                        dim3(kRouterWaves * kWave), 0, as_stream(stream), logits, indices, d_scores,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), norm_topk_prob ? 1 : 0,
-                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), nullptr, nullptr, nullptr, bf16_terms);
+                       d_add, nullptr, static_cast<bf16_t*>(d_logits_bf16), token_weight, stats, d_aux, bf16_terms);
   });
   return launch_status(name);
 }
@@ -963,15 +966,16 @@ int topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_sc
 extern "C" int moe_router_topk_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,
                                         const float* d_add, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
                                         void* d_logits_bf16, void* stream) {
-  return topk_bwd_bf16(logits, indices, d_scores, d_add, T, E, k, norm_topk_prob, d_logits_bf16, 0, stream,
-                       "moe_router_topk_bwd_bf16");
+  return topk_bwd_bf16(logits, indices, d_scores, d_add, nullptr, nullptr, nullptr, T, E, k, norm_topk_prob,
+                       d_logits_bf16, 0, stream, "moe_router_topk_bwd_bf16");
 }
 
 extern "C" int moe_router_bf16_logits_bwd(const float* logits, const int64_t* indices, const float* d_scores,
-                                          const float* d_logits, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
+                                          const float* d_logits, const float* token_weight, const float* stats,
+                                          const float* d_aux, int64_t T, int64_t E, int64_t k, int norm_topk_prob,
                                           void* d_logits_bf16, void* stream) {
-  return topk_bwd_bf16(logits, indices, d_scores, d_logits, T, E, k, norm_topk_prob, d_logits_bf16, 1, stream,
-                       "moe_router_bf16_logits_bwd");
+  return topk_bwd_bf16(logits, indices, d_scores, d_logits, token_weight, stats, d_aux, T, E, k, norm_topk_prob,
+                       d_logits_bf16, 1, stream, "moe_router_bf16_logits_bwd");
 }
 
 extern "C" int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indices, const float* d_scores,

@@ -208,10 +208,11 @@ def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tenso
     # Only the bf16 d_logits feeds the GEMMs; the incoming logits gradient is
     # read, not copied.
     if bf16_logits:
-        if d_aux is not None:
-            raise ValueError("the bf16-logit router's backward takes the aux loss's gradient as d_logits")
-        call("moe_router_bf16_logits_bwd", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
-             int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
+        tw = None if (d_aux is None or token_weight is None) else token_weight.float().contiguous()
+        da = None if d_aux is None else d_aux.float().reshape(1).contiguous()
+        call("moe_router_bf16_logits_bwd", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), ptr(tw),
+             ptr(stats if d_aux is not None else None), ptr(da), T, E, k, int(norm_topk_prob), ptr(dl_bf16), s,
+             tag="router_topk_bwd")
     elif d_aux is not None:
         tw = None if token_weight is None else token_weight.float().contiguous()
         da = d_aux.float().reshape(1).contiguous()
@@ -444,9 +445,13 @@ def router_aux_fwd(x: Tensor, weight: Tensor, top_k: int, norm_topk_prob: bool, 
     return _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias)
 
 
-def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias):
+def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bias, bf16_logits=False):
+    """(logits f32, scores f32, indices, aux, stats), plus the bf16 logits when
+    ``bf16_logits`` (``logits`` then holds their values in fp32)."""
     _require_gpu(x, weight, token_weight)
     if x.dtype == weight.dtype == torch.float32:
+        if bf16_logits:
+            raise ValueError("bf16 router logits need bf16 hidden states and router weight")
         # fp32 modules: the fp32 router, then the aux kernels on its logits
         logits, scores, idx = _router_fwd_f32(x.contiguous(), weight.contiguous(), top_k, norm_topk_prob, logit_bias)
         T, E = logits.shape
@@ -471,9 +476,13 @@ def _router_aux_kernels(x, weight, top_k, norm_topk_prob, token_weight, logit_bi
     stats = torch.empty(E + 1, dtype=torch.float32, device=dev)
     bias = None if logit_bias is None else logit_bias.to(device=dev, dtype=torch.float32).contiguous()
     tw = None if token_weight is None else token_weight.float().contiguous()
+    logits_b = torch.empty(T, E, dtype=BF16, device=dev) if bf16_logits else None
     ws = _ws(_lib.load().moe_router_aux_fwd_workspace_bytes(T, H, E), dev)
-    call("moe_router_aux_fwd", ptr(x), ptr(weight), ptr(bias), ptr(tw), ptr(logits), None, ptr(scores), ptr(idx), T,
-         H, E, top_k, int(norm_topk_prob), ptr(aux), ptr(stats), ptr(ws), ws.numel(), _stream(x), tag="router_fwd")
+    call("moe_router_aux_fwd", ptr(x), ptr(weight), ptr(bias), ptr(tw), ptr(logits), ptr(logits_b), ptr(scores),
+         ptr(idx), T, H, E, top_k, int(norm_topk_prob), ptr(aux), ptr(stats), ptr(ws), ws.numel(), _stream(x),
+         tag="router_fwd")
+    if bf16_logits:
+        return logits, scores, idx, aux, stats, logits_b
     return logits, scores, idx, aux, stats
 
 
@@ -871,22 +880,32 @@ def _refuse_traced_accumulation(accumulate_grad: bool, what: str) -> None:
 @torch.library.custom_op(f"{LIB}::moe_block_fwd", mutates_args=())
 def moe_block_fwd(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj: Tensor, top_k: int,
                   norm_topk_prob: bool, token_weight: Tensor | None = None, logit_bias: Tensor | None = None,
-                  accumulate_grad: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
-                                                          Tensor, Tensor, Tensor, Tensor, Tensor]:
+                  accumulate_grad: bool = False, bf16_logits: bool = False
+                  ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                             Tensor]:
     """router_aux_fwd then experts_fwd on its routes: (out, logits, scores,
-    indices, aux, stats, and experts_fwd's saved tensors)."""
-    logits, scores, idx, aux, stats = _router_aux_kernels(x, router_weight, top_k, norm_topk_prob, token_weight,
-                                                          logit_bias)
+    indices, aux, stats, and experts_fwd's saved tensors).  With
+    ``bf16_logits`` the logits and scores are bf16 (the router under bf16
+    autocast); the experts read the scores' values."""
+    if bf16_logits:
+        _, scores, idx, aux, stats, logits = _router_aux_kernels(x, router_weight, top_k, norm_topk_prob,
+                                                                 token_weight, logit_bias, True)
+    else:
+        logits, scores, idx, aux, stats = _router_aux_kernels(x, router_weight, top_k, norm_topk_prob, token_weight,
+                                                              logit_bias)
     out, xp, pre, act, y, pos, offsets = _experts_fwd_kernels(x, idx, scores, gate_up_proj, down_proj)
+    if bf16_logits:
+        scores = scores.to(BF16)  # bf16 values: the cast is exact
     return out, logits, scores, idx, aux, stats, xp, pre, act, y, pos, offsets
 
 
 @moe_block_fwd.register_fake
 def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, token_weight=None, logit_bias=None,
-      accumulate_grad=False):
+      accumulate_grad=False, bf16_logits=False):
     T, H = x.shape
     E = router_weight.shape[0]
-    router = (x.new_empty(T, E, dtype=torch.float32), x.new_empty(T, top_k, dtype=torch.float32),
+    rdt = BF16 if bf16_logits else torch.float32
+    router = (x.new_empty(T, E, dtype=rdt), x.new_empty(T, top_k, dtype=rdt),
               x.new_empty(T, top_k, dtype=torch.int64), x.new_empty((), dtype=torch.float32),
               x.new_empty(E + 1, dtype=torch.float32))
     out, xp, pre, act, y, pos, offsets = _experts_fake(x, top_k, gate_up_proj)
@@ -904,10 +923,11 @@ def _experts_fake(x, top_k, gate_up_proj):
 
 def _block_setup(ctx, inputs, output):
     ctx.set_materialize_grads(False)
-    x, rw, gu, dn, top_k, norm, token_weight, _bias, accumulate_grad = inputs
+    x, rw, gu, dn, top_k, norm, token_weight, _bias, accumulate_grad, bf16_logits = inputs
     _, logits, scores, idx, _, stats, xp, pre, act, y, pos, offsets = output
     ctx.save_for_backward(x, rw, gu, dn, logits, scores, idx, token_weight, stats, xp, pre, act, y, pos, offsets)
     ctx.norm = norm
+    ctx.bf16_logits = bf16_logits
     ctx.x_dtype = x.dtype
     ctx.params = (rw, gu, dn) if accumulate_grad else None
     ctx.mark_non_differentiable(idx, stats, xp, pre, act, y, pos, offsets)
@@ -916,7 +936,7 @@ def _block_setup(ctx, inputs, output):
 def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
     x, rw, gu, dn, logits, scores, idx, tw, stats, xp, pre, act, y, pos, offsets = ctx.saved_tensors
     if d_out is None and d_logits is None and d_scores is None and d_aux is None:
-        return (None,) * 9
+        return (None,) * 10
     targets = [_grad_target(p) for p in ctx.params] if ctx.params is not None else [None, None, None]
     # the router's weight gradient is added in place into a .grad of its own dtype
     rw_target = targets[0] if targets[0] is not None and targets[0].dtype == rw.dtype else None
@@ -927,10 +947,18 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
     def router_backward(d_w):
         # The routing weights' gradient from the experts plus any the scores
         # received elsewhere; the router's dX then joins d_hidden inside the
-        # permute backward instead of a separate add.
-        ds = d_w if d_scores is None else d_w + d_scores.float()
-        dx_router, grads["router"] = router_bwd_kernels(x, rw, logits, idx, d_logits, ds, ctx.norm, tw, stats, d_aux,
-                                                        rw_target)
+        # permute backward instead of a separate add.  bf16 scores have a
+        # bf16 gradient, which autograd sums in bf16 (the router kernel
+        # rounds d_w itself when nothing else is added).
+        if d_scores is None:
+            ds = d_w
+        elif ctx.bf16_logits:
+            ds = (d_w.to(BF16) + d_scores.to(BF16)).float()
+        else:
+            ds = d_w + d_scores.float()
+        lg = logits.float() if ctx.bf16_logits else logits
+        dx_router, grads["router"] = router_bwd_kernels(x, rw, lg, idx, d_logits, ds, ctx.norm, tw, stats, d_aux,
+                                                        rw_target, bf16_logits=ctx.bf16_logits)
         return dx_router
 
     params = {"gate_up_proj": (gu, targets[1]), "down_proj": (dn, targets[2])}
@@ -949,7 +977,7 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
         d_out = torch.zeros_like(x)
     dx, _d_w, d_gu, d_dn = experts_bwd_kernels(d_out, scores, gu, dn, xp, pre, act, y, pos, offsets, wgrad,
                                               on_d_weights=router_backward)
-    return dx.to(ctx.x_dtype), grads["router"], d_gu, d_dn, None, None, None, None, None
+    return dx.to(ctx.x_dtype), grads["router"], d_gu, d_dn, None, None, None, None, None, None
 
 
 moe_block_fwd.register_autograd(_block_backward, setup_context=_block_setup)
@@ -957,9 +985,17 @@ moe_block_fwd.register_autograd(_block_backward, setup_context=_block_setup)
 
 def moe_block(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj: Tensor, top_k: int,
               norm_topk_prob: bool, token_weight: Tensor | None = None, logit_bias: Tensor | None = None,
-              accumulate_grad: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+              accumulate_grad: bool = False, bf16_logits: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor,
+                                                                                 Tensor]:
     """Qwen3MoeSparseMoeBlock's router, experts and Switch aux loss as one op:
     (out [T,H], router_logits [T,E] fp32, scores [T,k], indices [T,k], aux).
+
+    ``bf16_logits`` runs the router as the reference does under bf16 autocast
+    (parallel/parallel/engine/engine.py:141): the logits of a bf16 linear,
+    softmax, top-k and the aux loss in fp32 on them, bf16 logits and scores
+    returned, and a backward that sums the logits' and scores' gradients in
+    bf16, as autograd does for bf16 tensors (``router_fwd_bf16``'s
+    semantics).
 
     The same results as ``router_aux_fwd`` followed by ``experts`` (TF
     modeling_qwen3_moe.py:249-267 and integrations/moe.py:377-478, the aux
@@ -973,7 +1009,7 @@ def moe_block(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj:
     hooks for those weights, refused under ``torch.compile``)."""
     _refuse_traced_accumulation(accumulate_grad, "moe_block")
     out, logits, scores, idx, aux = moe_block_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
-                                                  token_weight, logit_bias, accumulate_grad)[:5]
+                                                  token_weight, logit_bias, accumulate_grad, bf16_logits)[:5]
     return out, logits, scores, idx, aux
 
 

@@ -266,7 +266,7 @@ def test_bf16_logit_router_backward_sums_its_logit_gradients_in_bf16():
     d_add = la.grad.float()
     got = torch.empty(T, E, dtype=BF, device=DEV)
     _lib.call("moe_router_bf16_logits_bwd", logits32.data_ptr(), idx.data_ptr(), (ds := d_scores.float().to(DEV)).data_ptr(),
-              (da := d_add.to(DEV)).data_ptr(), T, E, k, 0, got.data_ptr(), _lib.stream_of(got))
+              (da := d_add.to(DEV)).data_ptr(), None, None, None, T, E, k, 0, got.data_ptr(), _lib.stream_of(got))
     torch.cuda.synchronize()
     got, want = got.cpu(), lb.grad
     lf = logits_b.cpu().float().requires_grad_()
@@ -280,3 +280,43 @@ def test_bf16_logit_router_backward_sums_its_logit_gradients_in_bf16():
     assert (got == want).float().mean() >= 0.999
     once = (lf.grad + d_add).to(BF)
     assert (once != want).float().mean() > 0.01, "the test data must separate one rounding from two"
+
+
+def test_moe_block_bf16_logits_c2_routes_bit_exactly_and_matches_the_separate_ops():
+    """ops.moe_block(bf16_logits=True) on the C2 layer (4096 tokens, H 2048,
+    128 experts, top-8), the router as the reference runs it under bf16
+    autocast (parallel/parallel/engine/engine.py:141): bf16 logits and
+    scores, the routing bit-exact on those logits (largest first, equal
+    logits in increasing expert index; the reference's fp32 softmax,
+    renormalisation and bf16 cast, TF modeling_qwen3_moe.py:258-267); the
+    same logits, scores, routes and output bits as router_fwd_bf16 followed
+    by the experts, the aux loss of load_balancing_loss_func on the bf16
+    logits, and the same gradients (the expert weights' bit for bit)."""
+    from parallel_amd import load_balancing_loss_func
+
+    w = WORKLOADS["c2"]
+    inp = make_block_inputs(w, seed=53, device=DEV, dtype=BF, weights_on_device_rng=True)
+    k, E = w.top_k, w.experts
+    coef = torch.tensor(w.aux_coef, device=DEV)
+    a = [inp[n].detach().clone().requires_grad_() for n in ("x", "router_weight", "gate_up_proj", "down_proj")]
+    out, lg, sc, idx, aux = ops.moe_block(*a, k, w.norm_topk_prob, bf16_logits=True)
+    assert lg.dtype == BF and sc.dtype == BF
+    lb = lg.detach().cpu()
+    canon = torch.argsort(-lb.float(), dim=-1, stable=True)[:, :k]
+    assert torch.equal(idx.cpu(), canon)
+    top = torch.softmax(lb.float(), dim=-1).gather(1, canon)
+    assert torch.equal(sc.detach().cpu(), (top / top.sum(dim=-1, keepdim=True)).to(BF))
+    b = [inp[n].detach().clone().requires_grad_() for n in ("x", "router_weight", "gate_up_proj", "down_proj")]
+    lg2, sc2, idx2, _ = ops.router_fwd_bf16(b[0], b[1], k, w.norm_topk_prob)
+    assert torch.equal(lg2, lg) and torch.equal(sc2, sc) and torch.equal(idx2, idx)
+    out2 = ops.experts(b[0], idx2, sc2, b[2], b[3])
+    assert torch.equal(out2, out)
+    aux2 = load_balancing_loss_func((lg2,), E, k)
+    torch.testing.assert_close(aux, aux2, rtol=1e-6, atol=0)
+    d_out = inp["d_out"]
+    torch.autograd.backward([out, aux], [d_out, coef])
+    torch.autograd.backward([out2, aux2], [d_out, coef])
+    torch.cuda.synchronize()
+    for name, ga, gb in zip(("dx", "d_router", "d_gate_up", "d_down"), a, b):
+        close_bf16(ga.grad, gb.grad, f"c2 bf16-logit block {name}")
+    assert torch.equal(a[2].grad, b[2].grad) and torch.equal(a[3].grad, b[3].grad)
