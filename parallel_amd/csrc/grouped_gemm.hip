@@ -206,6 +206,10 @@ using SmallTile = TileCfg<128, 128, 32, 2, 2, 5>;
 // The 256x256 loop with the fragment reads of each 16-deep half step
 // overlapping the previous half step's MFMAs.
 using BigTileP = TileCfg<256, 256, 32, 2, 4, 5, 1>;
+// Experts of up to 320 rows in one m-tile: 320x256 tiles (five 32-row
+// sub-tiles per wave, 160 accumulator registers per lane), A staged as 384
+// rows, 4-deep ring of 40 KiB stages.
+using WideTile = TileCfg<320, 256, 32, 2, 4, 4>;
 // Ping-pong on 256x256 tiles: waves 0-3 (one per SIMD) own output columns
 // 0-127, waves 4-7 columns 128-255; wave w and wave w + 4 share a SIMD.
 using PingTile = TileCfg<256, 256, 32, 2, 4, 5, 2>;
@@ -299,7 +303,12 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   constexpr int SN = WTN / 32;  // ... along N
   constexpr bool A_KC = (MODE == MODE_MG);
   constexpr bool B_KC = (MODE == MODE_MG) && B_KCONTIG;
-  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  // A K-contiguous A tile occupies whole rounds of DMA instructions in LDS
+  // (512 / BK rows per instruction, one instruction per wave per round): rows
+  // past BM are never read and their DMA is out of range (zeros, no traffic).
+  constexpr int A_ROWS = (MODE == MODE_MG) ? (BM + (512 / BK) * NWAVES - 1) / ((512 / BK) * NWAVES) * ((512 / BK) * NWAVES)
+                                           : BM;
+  constexpr int A_BYTES = A_ROWS * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   constexpr int NI_A = A_BYTES / 1024, NI_B = B_BYTES / 1024;  // DMA instructions per k-tile
   // Ping-pong: the DMA of a k-tile is split by operand between the wave
@@ -1292,6 +1301,9 @@ int launch(GemmParams& p, hipStream_t stream, const char* name) {
 // ping-pong loop (C4, 1024: the four row-grouped GEMMs 2769 against 2844 us;
 // C5, 512: 5297 against 5465 us; C2, 256: up_fwd 312 against 305 us).
 constexpr int64_t kPingMinMeanRows = 448;
+// Mean rows per expert up to which the expert GEMMs with wide outputs take
+// 320-row tiles.
+constexpr int64_t kWideMaxMeanRows = 288;
 
 // Expert GEMM over grouped rows.  256x256 tiles do the most MFMA work per
 // k-step of LDS traffic, but with few output columns their grid (about one
@@ -1308,12 +1320,19 @@ int launch_expert(GemmParams& p, hipStream_t stream, const char* name) {
   constexpr int64_t kTallMaxMeanRows = 288;
   if (out_cols <= 1024 && static_cast<int64_t>(p.rows) <= kTallMaxMeanRows * p.G)
     return launch<MODE_MG, B_KCONTIG, EPI, TallTile>(p, stream, name);
+  // A training step's routing (about 256 rows per expert, a few above):
+  // with 320-row tiles every expert of up to 320 rows is one m-tile, so its
+  // weights stream through one CU's LDS per n-tile instead of two (C2:
+  // up_fwd 280 against 318 us, down_fwd 155 against 167, up_dgrad 248
+  // against 272 on ping-pong).
+  if (static_cast<int64_t>(p.rows) <= kWideMaxMeanRows * p.G)
+    return launch<MODE_MG, B_KCONTIG, EPI, WideTile>(p, stream, name);
   // The ping-pong loop keeps the matrix pipes fed while the partner waves
   // read fragments and fire the DMA.  It wins for the input gradients (two
-  // transpose reads per weight fragment) at every size, and for the forward
-  // GEMMs once the experts average several m-tiles (their weight tiles then
-  // come from L2); with one or two m-tiles per expert the forward GEMMs
-  // stream every weight k-slice from HBM and time the same on both loops.
+  // transpose reads per weight fragment), and for the forward GEMMs once the
+  // experts average several m-tiles (their weight tiles then come from L2);
+  // with one or two m-tiles per expert the forward GEMMs stream every weight
+  // k-slice from HBM and time the same on both loops.
   if (!B_KCONTIG || static_cast<int64_t>(p.rows) >= kPingMinMeanRows * p.G)
     return launch<MODE_MG, B_KCONTIG, EPI, PingTile>(p, stream, name);
   return launch<MODE_MG, B_KCONTIG, EPI, BigTileP>(p, stream, name);

@@ -255,6 +255,8 @@ GEMM_CASES = [
     ("ping", [900, 0, 1100, 17, 513, 2000], 1536, 2048),
     ("ping_ragged", [1700, 3, 0, 640, 70], 200, 72),  # ragged n-tile, K tail inside the third k-tile
     ("ping_shortk", [520, 480, 33], 264, 40),  # two k-tiles (one nearly empty) per tile
+    # at most 288 rows per expert on average and wide outputs: 320-row tiles (exactly one and two full m-tiles)
+    ("wide", [320, 319, 1, 0, 640, 100, 33], 1536, 256),
 ]
 
 
