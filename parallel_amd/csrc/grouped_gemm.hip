@@ -214,9 +214,6 @@ using WideTile = TileCfg<320, 256, 32, 2, 4, 4>;
 // 0-127, waves 4-7 columns 128-255; wave w and wave w + 4 share a SIMD.
 using PingTile = TileCfg<256, 256, 32, 2, 4, 5, 2>;
 
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
-
 // A wave-uniform pointer moved to scalar registers (buffer resources must be).
 template <class T>
 __device__ __forceinline__ T* uniform_ptr(T* ptr) {
@@ -937,7 +934,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
   // groups of a weight gradient) are written out here directly: zeros, or
   // nothing when accumulating.  Returns false past the last tile.
   int relax = 0;  // steps whose tile wait still leaves the last epilogue's stores in flight
-  auto compute_seek = [&](int j) -> bool __attribute__((always_inline)) {
+  auto compute_seek = [&](int j) __attribute__((always_inline)) -> bool {
     for (;; ++j) {
       if (j >= ntiles) return false;
       if ((j >> 6) != cchunk) {

@@ -1177,9 +1177,345 @@ extern "C" int moe_router_aux_fwd(const void* x, const void* wr, const float* lo
   return aux_reduce_finalize(aux_ws, token_blocks(T, E), E, stats, aux, st, "moe_router_aux_fwd(reduce)");
 }
 
+// ---------------------------------------------------------------------------
+// The router's backward GEMMs in one pass, for E <= 128 experts (E a multiple
+// of 32): dX = dZ . Wr and the split-K partials of dWr = dZ^T . X.
+//
+// Both products have H as their column dimension and read the same dZ rows.
+// A block takes an HN-column slice of H and a chunk of the tokens, and walks
+// the chunk 64 tokens at a time: the sub-step's dZ rows (all experts) times
+// the block's Wr slice give its dX columns, and dZ^T times the sub-step's X
+// slice adds to the block's dWr partial.  dZ is read from L2 once per column
+// slice (1 MB at T 4096), X and dX once, the Wr slice once per block.  The
+// partials, one fp32 [E, H] plane per token chunk, are added in chunk order by
+// reduce_partials_bf16_kernel.
+//
+// MFMAs are v_mfma_f32_16x16x32_bf16 (A: 16 rows x 32 k, lane l holding row
+// l % 16, k 8 (l / 16) .. + 7; B likewise by column; D: lane l holds column
+// l % 16, rows 4 (l / 16) .. + 3).  dX is formed transposed, A = the Wr slice
+// read as [h][e] and B = the dZ rows, so that each lane's result is 4
+// consecutive columns of one token row (8-byte stores).  dWr takes A = dZ^T
+// and B = the X slice, both read with ds_read_b64_tr_b16 from their
+// token-major tiles: 16 lanes read a 4 (k) x 16 patch, lane i the 4 values of
+// row i / 4 at columns 4 (i % 4) .., and each receives the 4 k of column i.
+//
+// Eight waves in two groups of four (waves w and w + 4 share a SIMD): group g
+// takes the sub-steps of parity g, so that one group's MFMAs run while the
+// other's LDS reads and DMA are in flight.  Within a group, wave r computes
+// dX for tokens 16 r .. + 15 of its sub-step (all HN columns) and the dWr
+// rows 32 r .. + 31 (experts) x HN columns.  The groups' dWr sums are added
+// through LDS at the end, group 0's first.
+//
+// LDS: a ring of kRbStages sub-step stages, each a dZ tile [64 tokens][128
+// experts] (256-byte rows, 16-byte chunk c of row r at slot c ^ rb_zsw(r)) and
+// an X tile [64 tokens][HN] (chunk c of row r at slot c ^ rb_xsw<HN>(r)),
+// filled by LDS DMA (1 KiB instructions, lane l -> bytes 16 l ..: each lane
+// loads the global chunk that belongs at its slot).  Group g's four waves
+// load the sub-steps group g computes.  The Wr slice [128 experts][HN], in the
+// X tile's layout, first occupies the two stages the prologue leaves empty and
+// is read once into the dX A registers.  With these swizzles the 16 lanes of
+// a ds_read_b128 pass and the 32 lanes of a transpose-read pass touch 64
+// distinct banks.
+namespace moe {
+
+constexpr int kRbTok = 64;            // tokens per sub-step
+constexpr int kRbStages = 6;          // ring depth in sub-steps (3 iterations of 2)
+constexpr int kRbWaves = 8;
+constexpr int kRbE = 128;             // expert rows of the LDS tiles
+constexpr int kRbTargetBlocks = 256;  // one block per CU of an MI355X
+
+__device__ __forceinline__ int rb_zsw(int r) {
+  r &= 15;
+  return ((r & 3) << 2) | (((r >> 3) & 1) << 1) | ((r >> 2) & 1);
+}
+template <int HN>
+__device__ __forceinline__ int rb_xsw(int r) {
+  return HN == 32 ? 2 * ((r >> 3) & 1) : 2 * ((r >> 1) & 1) + 4 * ((r >> 3) & 1);
+}
+
+template <int HN, int S>
+struct RbCfg {
+  static_assert(HN == 32 || HN == 64, "column slices of 32 or 64");
+  static_assert(S % 2 == 0 && S >= 6, "whole iterations, two of them prefetched");
+  static constexpr int kCpr = HN / 8;                // 16-byte chunks per X / Wr row
+  static constexpr int kRowsPerInst = 1024 / (HN * 2);
+  static constexpr int kZBytes = kRbTok * kRbE * 2;  // 16 KiB
+  static constexpr int kXBytes = kRbTok * HN * 2;
+  static constexpr int kStage = kZBytes + kXBytes;
+  static constexpr int kWBytes = kRbE * HN * 2;
+  static constexpr int kZInst = kZBytes / 1024 / 4;  // per wave of the loading group
+  static constexpr int kXInst = kXBytes / 1024 / 4;
+  static constexpr int kWInst = kWBytes / 1024 / kRbWaves;  // the Wr slice, all eight waves
+  static constexpr int kInst = kZInst + kXInst;
+  static constexpr int kMT = HN / 16;  // 16-column tiles
+  static constexpr int kAhead = S / 2 - 1;  // iterations in flight beyond the current one
+  static constexpr int kLds = S * kStage;
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert(kWBytes <= (S - 2 * kAhead) * kStage, "the Wr slice fits the stages the prologue leaves empty");
+  static_assert(4 * (2 * kMT * 4) * 64 * 4 <= kLds, "group 1's dWr sums fit the drained ring");
+};
+
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+// vmcnt at the end of iteration i: the DMA of the wave's next sub-step (next
+// iteration) has landed when at most the younger DMA (A - 1 iterations of NI
+// instructions) and the dX stores of the last min(i + 1, A) iterations (MT
+// each) are outstanding.
+template <int A, int NI, int MT, int C = 1>
+__device__ __forceinline__ void rb_wait(int i) {
+  static_assert((A - 1) * NI + A * MT < 64, "vmcnt range");
+  if constexpr (C == A) {
+    wait_vmcnt<(A - 1) * NI + C * MT>();
+  } else {
+    if (i + 1 == C) wait_vmcnt<(A - 1) * NI + C * MT>();
+    else rb_wait<A, NI, MT, C + 1>(i);
+  }
+}
+
+template <int HN, int S>
+__global__ __launch_bounds__(kRbWaves * kWave) void router_bwd_gemm_kernel(
+    const bf16_t* __restrict__ dz, const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr,
+    bf16_t* __restrict__ dx, float* __restrict__ partials, int T, int H, int E, int tchunk, int nh) {
+  using C = RbCfg<HN, S>;
+  constexpr int ZI = C::kZInst, XI = C::kXInst, WI = C::kWInst, NI = C::kInst, MT = C::kMT, A = C::kAhead;
+  constexpr int RPI = C::kRowsPerInst;
+  constexpr uint32_t kOut = 0x80000000u;  // >= every resource size (checked on the host)
+  __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
+  char* const wtile = lds + 2 * A * C::kStage;  // stages 2 A .. (empty until iteration 0 refills them)
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int grp = wave >> 2, rw = wave & 3;
+  const int q = lane >> 4, i16 = lane & 15;
+  // Block -> (column slice, token chunk).  Launch indices are dealt to the 8
+  // XCDs in turn; each XCD takes a run of consecutive column slices (all
+  // their chunks), so the two blocks writing the halves of a 128-byte dX line
+  // (HN 32) share an L2.
+  const int nb = gridDim.x;
+  int b = blockIdx.x;
+  if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
+  const int ns = nb / nh;
+  const int sp = b % ns, hb = b / ns;
+  const int h0 = hb * HN;
+  const int tb = sp * tchunk, te = min(T, tb + tchunk);
+  const int nit = (te - tb + 2 * kRbTok - 1) / (2 * kRbTok);  // iterations of two sub-steps
+  const u32x4_t rz = rsrc_words(dz, static_cast<uint32_t>(T) * static_cast<uint32_t>(E) * 2u);
+  const u32x4_t rx = rsrc_words(x, static_cast<uint32_t>(T) * static_cast<uint32_t>(H) * 2u);
+  const u32x4_t rwr = rsrc_words(wr, static_cast<uint32_t>(E) * static_cast<uint32_t>(H) * 2u);
+  const __amdgpu_buffer_rsrc_t rdx =
+      __builtin_amdgcn_make_buffer_rsrc(dx, 0, static_cast<int>(static_cast<uint32_t>(T) * H * 2u), 0x00020000);
+  const uint32_t ring = lds_address(lds);
+  // This lane's tile row and global column bytes in each of its DMA
+  // instructions of a stage (kOut: a chunk past E).
+  int zrow[ZI], xrow[XI];
+  uint32_t zcol[ZI], xcol[XI];
+#pragma unroll
+  for (int j = 0; j < ZI; ++j) {
+    const int r = 4 * (ZI * rw + j) + q;
+    const int c = i16 ^ rb_zsw(r);
+    zrow[j] = r;
+    zcol[j] = c < E / 8 ? static_cast<uint32_t>(c) * 16u : kOut;
+  }
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int r = RPI * (XI * rw + j) + lane / C::kCpr;
+    const int c = (lane % C::kCpr) ^ rb_xsw<HN>(r);
+    xrow[j] = r;
+    xcol[j] = static_cast<uint32_t>(h0 + 8 * c) * 2u;
+  }
+  // This group's sub-step of iteration it into its stage; past the chunk
+  // every lane reads zeros.
+  auto issue = [&](int it) __attribute__((always_inline)) {
+    const int ss = 2 * it + grp;
+    const int t0 = tb + ss * kRbTok;
+    const uint32_t base = ring + (ss % S) * C::kStage;
+#pragma unroll
+    for (int j = 0; j < ZI; ++j) {
+      const int t = t0 + zrow[j];
+      const uint32_t off = (t < te && zcol[j] != kOut)
+                               ? static_cast<uint32_t>(t) * static_cast<uint32_t>(E) * 2u + zcol[j]
+                               : kOut;
+      dma16(rz, off, __builtin_amdgcn_readfirstlane(base + (ZI * rw + j) * 1024));
+    }
+#pragma unroll
+    for (int j = 0; j < XI; ++j) {
+      const int t = t0 + xrow[j];
+      const uint32_t off = t < te ? static_cast<uint32_t>(t) * static_cast<uint32_t>(H) * 2u + xcol[j] : kOut;
+      dma16(rx, off, __builtin_amdgcn_readfirstlane(base + C::kZBytes + (XI * rw + j) * 1024));
+    }
+  };
+  // The Wr slice (expert rows past E read as zeros), then A iterations.
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int r = RPI * (WI * wave + j) + lane / C::kCpr;
+    const int c = (lane % C::kCpr) ^ rb_xsw<HN>(r);
+    const uint32_t off = r < E ? static_cast<uint32_t>(r) * static_cast<uint32_t>(H) * 2u +
+                                     static_cast<uint32_t>(h0 + 8 * c) * 2u
+                               : kOut;
+    dma16(rwr, off, __builtin_amdgcn_readfirstlane(lds_address(wtile) + (WI * wave + j) * 1024));
+  }
+#pragma unroll
+  for (int it = 0; it < A; ++it) issue(it);
+  wait_vmcnt<(A - 1) * NI>();  // the Wr slice and iteration 0
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // Transpose-read address of (k-row kr, column col) in a [k-rows][cols]
+  // tile: the X / Wr layout (HN columns) or the dZ layout (128 columns).
+  auto xaddr = [&](int kr, int col) __attribute__((always_inline)) {
+    return kr * (HN * 2) + (((col >> 3) ^ rb_xsw<HN>(kr)) << 4) + (col & 7) * 2;
+  };
+  auto zaddr = [&](int kr, int col) __attribute__((always_inline)) {
+    return kr * 256 + (((col >> 3) ^ rb_zsw(kr)) << 4) + (col & 7) * 2;
+  };
+  auto tr8 = [&](const char* p, int off_lo, int off_hi) __attribute__((always_inline)) {
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + off_lo));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + off_hi));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  // Lane (q, i) of a transpose read takes k-row 8 q + 4 h + i / 4 of its
+  // 32-deep k-step and columns 4 (i % 4) .. of its 16-column tile.
+  const int tr_kr = 8 * q + (i16 >> 2), tr_col = 4 * (i16 & 3);
+  // dX^T A operand: Wr slice column tile m (h0 + 16 m ..), k-step ks (experts 32 ks ..).
+  bf16x8_t wa[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      wa[m][ks] = tr8(wtile, xaddr(32 * ks + tr_kr, 16 * m + tr_col), xaddr(32 * ks + tr_kr + 4, 16 * m + tr_col));
+  wait_lgkmcnt0();  // every wave's Wr reads are done before iteration 0 refills those stages
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  f32x4_t dw[2][MT];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int n = 0; n < MT; ++n) dw[mi][n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const bool dw_rows[2] = {32 * rw < E, 32 * rw + 16 < E};  // wave-uniform
+  const int zrow_b = 16 * rw + i16;  // this lane's token row of the dX^T B operand
+  for (int it = 0; it < nit; ++it) {
+    // Refill the stages of iteration it - 1: every wave finished reading them
+    // before the barrier that ended iteration it - 1.
+    issue(it + A);
+    const int ss = 2 * it + grp;
+    const char* zt = lds + (ss % S) * C::kStage;
+    const char* xt = zt + C::kZBytes;
+    // dX^T for the wave's 16 tokens: tile m holds columns h0 + 16 m + 4 q ..
+    // + 3 of token zrow_b.
+    f32x4_t ax[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) ax[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8_t bz =
+          *reinterpret_cast<const bf16x8_t*>(zt + zrow_b * 256 + (((4 * ks + q) ^ rb_zsw(zrow_b)) << 4));
+#pragma unroll
+      for (int m = 0; m < MT; ++m) ax[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[m][ks], bz, ax[m], 0, 0, 0);
+    }
+    // dWr rows 32 rw + 16 mi .. (experts) x columns 16 n .. over the 64 tokens.
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8_t za[2], xb[MT];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const int col = 32 * rw + 16 * mi + tr_col;
+        za[mi] = tr8(zt, zaddr(32 * ks + tr_kr, col), zaddr(32 * ks + tr_kr + 4, col));
+      }
+#pragma unroll
+      for (int n = 0; n < MT; ++n)
+        xb[n] = tr8(xt, xaddr(32 * ks + tr_kr, 16 * n + tr_col), xaddr(32 * ks + tr_kr + 4, 16 * n + tr_col));
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+        if (dw_rows[mi]) {
+#pragma unroll
+          for (int n = 0; n < MT; ++n) dw[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(za[mi], xb[n], dw[mi][n], 0, 0, 0);
+        }
+    }
+    // dX stores, issued by every lane (a token past the chunk stores out of
+    // range, which the hardware drops), so each iteration adds MT to vmcnt.
+    const int t = tb + ss * kRbTok + zrow_b;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint32_t off = t < te ? (static_cast<uint32_t>(t) * static_cast<uint32_t>(H) +
+                                     static_cast<uint32_t>(h0 + 16 * m + 4 * q)) * 2u
+                                  : kOut;
+      const u32x2_t v = u32x2_t{pack_bf16x2(ax[m][0], ax[m][1]), pack_bf16x2(ax[m][2], ax[m][3])};
+      __builtin_amdgcn_raw_buffer_store_b64(v, rdx, off, 0, 0);
+    }
+    rb_wait<A, NI, MT>(it);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  wait_vmcnt<0>();  // the trailing (zero) DMA has landed: the ring is free
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // Group 1 hands its dWr sums to group 0 through the ring (lane-major, so
+  // both sides address the same element), group 0 adds them to its own.
+  float* hand = reinterpret_cast<float*>(lds) + rw * (2 * MT * 4 * kWave) + lane;
+  if (grp == 1) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int n = 0; n < MT; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hand[((mi * MT + n) * 4 + i) * kWave] = dw[mi][n][i];
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  // dWr partial: lane holds column h0 + 16 n + i16 of expert rows 32 rw + 16 mi + 4 q ..
+  float* plane = partials + static_cast<int64_t>(sp) * E * H;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int n = 0; n < MT; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 32 * rw + 16 * mi + 4 * q + i;
+        const float v = dw[mi][n][i] + hand[((mi * MT + n) * 4 + i) * kWave];
+        if (e < E) plane[static_cast<int64_t>(e) * H + h0 + 16 * n + i16] = v;
+      }
+}
+
+}  // namespace moe
+
+namespace {
+bool router_bwd_fused(int64_t T, int64_t H, int64_t E) {
+  constexpr int64_t kMax = (1ll << 31) - 64;
+  return E <= kRbE && E % 32 == 0 && H % 32 == 0 && T * H * 2 < kMax && T * E * 2 < kMax && E * H * 2 < kMax;
+}
+// Column slice, token chunk and chunk count of the one-pass kernel: about
+// kRbTargetBlocks blocks.  32-column slices keep the chunks (and the fp32
+// partials) fewer; from 8192 tokens 64-column slices halve the passes over dZ
+// instead.  Entry point with its reduce, H 2048, E 128: T 4096 17.6 us (32)
+// against 20.1 us (64), T 16384 44.0 against 40.9 us, T 8192 / H 4096 43.4
+// against 40.3 us.
+void router_bwd_plan(int64_t T, int64_t H, int& hn, int& tchunk, int& splits) {
+  hn = (H % 64 == 0 && T >= 8192) ? 64 : 32;
+  const int64_t nh = H / hn;
+  int64_t want = (kRbTargetBlocks + nh / 2) / nh;
+  if (want < 1) want = 1;
+  int64_t tc = (T + want - 1) / want;
+  tc = (tc + kRbTok - 1) / kRbTok * kRbTok;
+  if (tc < kRbTok) tc = kRbTok;
+  tchunk = static_cast<int>(tc);
+  splits = static_cast<int>((T + tc - 1) / tc);
+}
+}  // namespace
+
 extern "C" size_t moe_router_logits_bwd_workspace_bytes(int64_t T, int64_t H, int64_t E) {
   if (T < 0 || H < 1 || E < 1) return 0;
-  int64_t chunks = (T + kRouterWgradChunk - 1) / kRouterWgradChunk;
+  int64_t chunks;
+  if (router_bwd_fused(T, H, E)) {
+    int hn, tchunk, splits;
+    router_bwd_plan(T, H, hn, tchunk, splits);
+    chunks = splits;
+  } else {
+    chunks = (T + kRouterWgradChunk - 1) / kRouterWgradChunk;
+  }
   if (chunks < 1) chunks = 1;
   return static_cast<size_t>(chunks) * static_cast<size_t>(E) * static_cast<size_t>(H) * sizeof(float);
 }
@@ -1198,10 +1534,31 @@ extern "C" int moe_router_logits_bwd(const void* d_logits_bf16, const void* x, c
   const size_t need = moe_router_logits_bwd_workspace_bytes(T, H, E);
   MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
               "router logits bwd: workspace %zu < %zu bytes", workspace_bytes, need);
-  const int chunks = static_cast<int>((T + kRouterWgradChunk - 1) / kRouterWgradChunk);
   float* partials = static_cast<float*>(workspace);
+  int chunks;
+  if (router_bwd_fused(T, H, E)) {
+    int hn, tchunk;
+    router_bwd_plan(T, H, hn, tchunk, chunks);
+    if (T > 0) {
+      const int nh = static_cast<int>(H / hn);
+      const dim3 grid(nh * chunks);
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(kRbWaves * kWave), 0, st, static_cast<const bf16_t*>(d_logits_bf16),
+                           static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), static_cast<bf16_t*>(dx),
+                           partials, static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), tchunk, nh);
+      };
+      if (hn == 64) go(router_bwd_gemm_kernel<64, kRbStages>);
+      else go(router_bwd_gemm_kernel<32, kRbStages>);
+      const int rc = launch_status("moe_router_logits_bwd(gemm)");
+      if (rc) return rc;
+    } else {
+      chunks = 0;  // no tokens: the reduction below writes a zero gradient
+    }
+  } else {
+    chunks = static_cast<int>((T + kRouterWgradChunk - 1) / kRouterWgradChunk);
+  }
   int rc;
-  if (T > 0) {  // with no tokens the reduction below writes a zero gradient
+  if (T > 0 && !router_bwd_fused(T, H, E)) {  // with no tokens the reduction below writes a zero gradient
     rc = router_dgrad(static_cast<const bf16_t*>(d_logits_bf16), static_cast<const bf16_t*>(wr),
                       static_cast<bf16_t*>(dx), static_cast<int>(T), static_cast<int>(H), static_cast<int>(E), st);
     if (rc) return rc;

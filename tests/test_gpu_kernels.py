@@ -59,10 +59,16 @@ def test_router_logits_match_fp32(T, H, E):
 
 
 # Many router weight-gradient partials, the last one ragged (512-row chunks:
-# 18 at 9000 tokens, 34 at 17000).
+# 18 at 9000 tokens, 34 at 17000).  E a multiple of 32 up to 128 with H a
+# multiple of 32 takes the one-pass kernel: 64-column slices (C2: 8 chunks of
+# 512 tokens; 9001 tokens: 29 chunks of 320, the last ragged), 32-column
+# slices (H 96, 160, 2080), experts past E read as zeros (E 32, 96), fewer
+# tokens than one 64-token sub-step (37).
 @pytest.mark.parametrize("T,H,norm,E,k", [(384, 256, True, 16, 4), (384, 256, False, 16, 4), (384, 256, True, 200, 6),
                                           (384, 256, False, 384, 1), (9000, 264, True, 128, 8),
-                                          (17000, 136, False, 64, 6)])
+                                          (17000, 136, False, 64, 6), (4096, 2048, True, 128, 8),
+                                          (9001, 512, True, 128, 8), (1000, 96, False, 96, 6), (37, 64, True, 32, 4),
+                                          (300, 160, False, 64, 6), (2000, 2080, True, 128, 8)])
 def test_router_backward_matches_autograd(T, H, norm, E, k):
     x = torch.randn(T, H, generator=gen(3)).to(BF)
     w = (torch.randn(E, H, generator=gen(4)) * 0.05).to(BF)
@@ -80,6 +86,47 @@ def test_router_backward_matches_autograd(T, H, norm, E, k):
     torch.autograd.backward([sr, lr], [d_scores, d_logits])
     close_bf16(xg.grad, xr.grad, "router dx")
     close_bf16(wg.grad, wr.grad, "router dweight")
+
+
+@pytest.mark.parametrize("T,H,E,accumulate", [(4096, 2048, 128, False), (9001, 512, 128, True), (1000, 96, 96, False),
+                                               (37, 64, 32, True), (2000, 2080, 128, False), (300, 264, 64, False)])
+def test_router_gemm_backward_is_the_exact_products(T, H, E, accumulate):
+    """moe_router_logits_bwd through the C ABI on given bf16 dZ, X and Wr:
+    every element of dX = dZ Wr and dWr = dZ^T X within one bf16 rounding of
+    the fp64 product plus an fp32-summation bound (2^-16 of the sum of the
+    terms' magnitudes), which a dropped token, sub-step or column tile
+    exceeds; with dwr_accumulate, dWr = bf16(old + bf16(sum)).  Covers the
+    one-pass kernel's 64- and 32-column slices, ragged token chunks and E < 128
+    (H 264 takes the two-kernel path)."""
+    g = gen(T + H)
+    dz = (torch.randn(T, E, generator=g) * 0.1).to(BF)
+    x = torch.randn(T, H, generator=g).to(BF)
+    w = (torch.randn(E, H, generator=g) * 0.05).to(BF)
+    old = (torch.randn(E, H, generator=g) * 0.01).to(BF)
+    dzd, xd, wd = dz.to(DEV), x.to(DEV), w.to(DEV)
+    dx = torch.full((T, H), float("nan"), dtype=BF, device=DEV)
+    dw = old.to(DEV) if accumulate else torch.full((E, H), float("nan"), dtype=BF, device=DEV)
+    lib = _lib.load()
+    ws = torch.empty(max(lib.moe_router_logits_bwd_workspace_bytes(T, H, E), 16), dtype=torch.uint8, device=DEV)
+    _lib.call("moe_router_logits_bwd", _lib.ptr(dzd), _lib.ptr(xd), _lib.ptr(wd), _lib.ptr(dx), _lib.ptr(dw),
+              int(accumulate), T, H, E, _lib.ptr(ws), ws.numel(), _lib.stream_of(dzd))
+    torch.cuda.synchronize()
+    a, b, c = dz.double(), x.double(), w.double()
+    for name, got, ref, mag, base in (("dX", dx, a @ c, a.abs() @ c.abs(), None),
+                                      ("dWr", dw, a.t() @ b, a.abs().t() @ b.abs(), old if accumulate else None)):
+        got = got.cpu().double()
+        fresh = ref.to(BF).double()
+        want = fresh if base is None else (base.double() + fresh).to(BF).double()
+        # One bf16 ulp of the product (the fp32 sum may round the other way),
+        # one of the accumulated result, and the fp32 summation error.
+        bound = ref.abs() * 2.0 ** -7 + mag * 2.0 ** -16 + 1e-30
+        if base is not None:
+            bound = bound + want.abs() * 2.0 ** -7
+        err = (got - want).abs()
+        assert torch.isfinite(got).all(), f"{name}: non-finite (unwritten) elements"
+        bad = err > bound
+        assert not bad.any(), (f"{name}: {int(bad.sum())} elements outside the bound, worst at "
+                               f"{np.unravel_index(int((err / bound).argmax()), tuple(err.shape))}")
 
 
 # ------------------------------------------------------------------ aux loss
