@@ -63,8 +63,8 @@ extern "C" int moe_permute_fwd_noalloc(const void* hidden, int64_t T, int64_t H,
   void* ws = nullptr;
   const int rc = scratch_of_current_device(&ws);
   if (rc) return rc;
-  // The count kernel stores every histogram entry that the scan and scatter
-  // kernels read, so nothing in the scratch has to start at zero.
+  // The count kernel stores every histogram entry that the scatter kernel
+  // reads, so nothing in the scratch has to start at zero.
   return moe::permute_fwd_run(hidden, T, H, ids, k, divisor, num_buckets, permuted, perm, pos_of_slot, counts,
                               offsets, ws, kScratchBytes, stream);
 }

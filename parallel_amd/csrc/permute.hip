@@ -1,19 +1,18 @@
 // Token permutation into expert-contiguous (or owner-rank-contiguous) order.
 //
 // A stable counting sort of the S = T*k routed slots by bucket = id / divisor,
-// in three small launches plus one bandwidth-bound row gather:
+// in two small launches plus one bandwidth-bound row gather:
 //   1. count:   each block histograms a CHUNK of slots in LDS (integer
 //               atomics, so counts are exact and order-free);
-//   2. scan:    one block turns the [blocks x buckets] histogram into
-//               per-bucket prefixes over the blocks, plus the per-bucket
-//               counts and inclusive offsets (a block's first position in a
-//               bucket is its prefix plus the bucket's start);
-//   3. scatter: each block re-walks its chunk 256 slots at a time; a wave
-//               finds equal keys with one ballot per key bit, ranks a slot by
-//               the popcount of equal-key lanes below it, and waves are
-//               ordered through per-round LDS counters, which keeps the sort
-//               stable;
-//   4. gather:  one wave per sorted row copies hidden[perm/k] (16-byte lanes).
+//   2. scatter: each block reads the [blocks x buckets] histogram for its
+//               prefix over the blocks before it and the buckets' totals
+//               (their scan gives the bucket starts; block 0 writes the
+//               per-bucket counts and inclusive offsets), then re-walks its
+//               chunk 256 slots at a time: a wave finds equal keys with one
+//               ballot per key bit, ranks a slot by the popcount of equal-key
+//               lanes below it, and waves are ordered through per-round LDS
+//               counters, which keeps the sort stable;
+//   3. gather:  one wave per sorted row copies hidden[perm/k] (16-byte lanes).
 // Sentinel slots (bucket >= num_buckets) land after every real bucket.
 //
 // Reference: TF/integrations/moe.py:389-437 (sort/gather/histc/cumsum,
@@ -61,75 +60,92 @@ __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(const int64
   for (int i = threadIdx.x; i < nb1; i += kPermThreads) hist[static_cast<int64_t>(blockIdx.x) * nb1 + i] = h[i];
 }
 
-// hist[b][e] (counts) -> the exclusive prefix over blocks b of bucket e, in
-// place; counts[e] and inclusive offsets[e] for the real buckets.  Block b's
-// first sorted position for bucket e is hist[b][e] + start(e), with start(e) =
-// offsets[e] - counts[e] (and offsets[nb - 1] for the sentinel bucket).
-__global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict__ hist, int nblk, int nb,
-                                                            int32_t* __restrict__ counts,
-                                                            int32_t* __restrict__ offsets) {
-  __shared__ int tot[kMaxBuckets + 1];
-  __shared__ int wsum[16];
-  const int nb1 = nb + 1;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1), wave = tid >> 6;
-  // Column prefix over blocks (per bucket), exclusive; 32 rows' loads in
-  // flight at a time.
-  constexpr int kRows = 32;
-  for (int e = tid; e < nb1; e += blockDim.x) {
-    int run = 0;
-    for (int b0 = 0; b0 < nblk; b0 += kRows) {
-      int c[kRows];
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) c[r] = b0 + r < nblk ? hist[static_cast<int64_t>(b0 + r) * nb1 + e] : 0;
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) {
-        if (b0 + r < nblk) hist[static_cast<int64_t>(b0 + r) * nb1 + e] = run;
-        run += c[r];
-      }
-    }
-    tot[e] = run;
-  }
-  __syncthreads();
-  // Inclusive scan over the real buckets (nb <= 1024: one pass).
-  const int v = tid < nb ? tot[tid] : 0;
-  const int incl = wave_inclusive_scan(v);
-  if (lane == kWave - 1) wsum[wave] = incl;
-  __syncthreads();
-  int wprefix = 0;
-  for (int w = 0; w < wave; ++w) wprefix += wsum[w];
-  if (tid < nb) {
-    counts[tid] = v;
-    offsets[tid] = wprefix + incl;
-  }
-}
-
+// Each block first places its chunk from the count kernel's histogram
+// hist[nblk][nb + 1]: per bucket, the counts of the blocks before it (its
+// first position within the bucket) and of all blocks (the bucket's size); an
+// exclusive scan of the sizes gives the buckets' starts, the sentinel bucket's
+// after every real one.  Block 0 also writes counts[e] and the inclusive
+// offsets[e] of the real buckets.  (One launch fewer than a separate scan
+// kernel; each block reads the nblk x (nb + 1) histogram from L2.)
 __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(const int64_t* __restrict__ ids, int S,
                                                                         int64_t divisor, int nb,
-                                                                        const int32_t* __restrict__ col_prefix,
-                                                                        const int32_t* __restrict__ counts,
-                                                                        const int32_t* __restrict__ offsets,
+                                                                        const int32_t* __restrict__ hist, int nblk,
+                                                                        int32_t* __restrict__ counts,
+                                                                        int32_t* __restrict__ offsets,
                                                                         int32_t* __restrict__ perm,
                                                                         int32_t* __restrict__ pos_of_slot) {
   __shared__ int running[kMaxBuckets + 1];
+  __shared__ int total[kMaxBuckets + 1];
   __shared__ int wave_cnt[kPermThreads / kWave][kMaxBuckets + 1];
+  __shared__ int wsum[kPermThreads / kWave];
   const int nb1 = nb + 1;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid >> 6;
   const int begin = blockIdx.x * kChunk;
   const int end = min(begin + kChunk, S);
   // Every round's ids in flight before the first round.
   int64_t id[kPerThread];
 #pragma unroll
   for (int r = 0; r < kPerThread; ++r) {
-    const int s = begin + r * kPermThreads + threadIdx.x;
+    const int s = begin + r * kPermThreads + tid;
     id[r] = s < end ? ids[s] : -1;
   }
-  for (int i = threadIdx.x; i < nb1; i += kPermThreads) {
-    const int bucket_start = i < nb ? offsets[i] - counts[i] : offsets[nb - 1];
-    running[i] = col_prefix[static_cast<int64_t>(blockIdx.x) * nb1 + i] + bucket_start;
+  // Per bucket: the blocks before this one, and all blocks; 32 rows' loads in
+  // flight at a time.
+  constexpr int kRows = 32;
+  const int me = static_cast<int>(blockIdx.x);
+  for (int e = tid; e < nb1; e += kPermThreads) {
+    int before = 0, all = 0;
+    for (int b0 = 0; b0 < nblk; b0 += kRows) {
+      int c[kRows];
 #pragma unroll
-    for (int w = 0; w < kPermThreads / kWave; ++w) wave_cnt[w][i] = 0;
+      for (int r = 0; r < kRows; ++r) c[r] = b0 + r < nblk ? hist[static_cast<int64_t>(b0 + r) * nb1 + e] : 0;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        before += b0 + r < me ? c[r] : 0;
+        all += c[r];
+      }
+    }
+    running[e] = before;
+    total[e] = all;
+#pragma unroll
+    for (int w = 0; w < kPermThreads / kWave; ++w) wave_cnt[w][e] = 0;
   }
+  __syncthreads();
+  // Buckets' starts: thread t scans the real buckets t G .. t G + G - 1
+  // (G = ceil(nb / kPermThreads) <= 4) in order, the threads in turn.
+  constexpr int kG = (kMaxBuckets + kPermThreads - 1) / kPermThreads;
+  const int G = (nb + kPermThreads - 1) / kPermThreads;
+  int size[kG];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const int e = tid * G + j;
+    size[j] = (j < G && e < nb) ? total[e] : 0;
+    sum += size[j];
+  }
+  const int incl = wave_inclusive_scan(sum);
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  int run = incl - sum, n_valid = 0;
+#pragma unroll
+  for (int w = 0; w < kPermThreads / kWave; ++w) {
+    run += w < wave ? wsum[w] : 0;
+    n_valid += wsum[w];
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const int e = tid * G + j;
+    if (j < G && e < nb) {
+      if (me == 0) {
+        counts[e] = size[j];
+        offsets[e] = run + size[j];
+      }
+      running[e] += run;
+      run += size[j];
+    }
+  }
+  if (tid == 0) running[nb] += n_valid;
   __syncthreads();
   int nbits = 1;
   while ((1 << nbits) < nb1) ++nbits;
@@ -331,14 +347,11 @@ int permute_fwd_run(const void* hidden, int64_t T, int64_t H, const int64_t* ids
     int rc = launch_status("moe_permute_fwd(count)");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, st, hist, nblk, nb, counts, offsets);
-  int rc = launch_status("moe_permute_fwd(scan)");
-  if (rc) return rc;
-  if (nblk == 0) return MOE_OK;
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nblk), dim3(kPermThreads), 0, st, ids, S, divisor, nb, hist, counts,
-                     offsets, perm, pos_of_slot);
-  rc = launch_status("moe_permute_fwd(scatter)");
-  if (rc) return rc;
+  // With no slots one block still writes the zero counts and offsets.
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nblk > 0 ? nblk : 1), dim3(kPermThreads), 0, st, ids, S, divisor, nb,
+                     hist, nblk, counts, offsets, perm, pos_of_slot);
+  int rc = launch_status("moe_permute_fwd(scatter)");
+  if (rc || nblk == 0) return rc;
   if (permuted) {
     MOE_DISPATCH_K(k, scatter_rows_kernel, dim3(row_grid(T)), dim3(kPermThreads), 0, st,
                    static_cast<const bf16_t*>(hidden), static_cast<int>(H), pos_of_slot, static_cast<int>(T),

@@ -206,6 +206,9 @@ PERMUTE_CASES = [
     dict(T=3000, k=4, E=64, seed=5, sentinel_frac=0.4),
     dict(T=700, k=3, E=1024, seed=6, distinct=False),
     dict(T=2049, k=1, E=2, seed=7, distinct=False),
+    # 262144 and 320000 routes: 512 and 625 count blocks in every scatter block's prefix
+    dict(T=32768, k=8, E=128, seed=8, skew=torch.linspace(0, 3, 128)),
+    dict(T=40000, k=8, E=128, seed=9, sentinel_frac=0.1),
 ]
 
 
