@@ -98,6 +98,7 @@ def read_traffic(tag: str, workload: str):
 _TAG_KERNELS = {
     "router_fused_fwd_kernel": "router_fwd",
     "router_reduce_topk_kernel": "router_fwd",
+    "router_bwd_gemm_kernel": "router_gemm_bwd",
     "reduce_partials_bf16_kernel": "router_gemm_bwd",
     "router_topk_bwd_kernel": "router_topk_bwd",
     "aux_partial_kernel": "aux_fwd",
@@ -105,7 +106,6 @@ _TAG_KERNELS = {
     "aux_finalize_kernel": "router_fwd",
     "aux_bwd_kernel": "aux_bwd",
     "permute_count_kernel": "permute_fwd",
-    "permute_scan_kernel": "permute_fwd",
     "permute_scatter_kernel": "permute_fwd",
     "scatter_rows_kernel": "permute_fwd",
     "combine_fwd_kernel": "combine_fwd",
