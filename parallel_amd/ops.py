@@ -54,21 +54,6 @@ def _stream(t: Tensor) -> int:
     return _lib.stream_of(t)
 
 
-_SIDE_STREAMS: dict = {}
-
-
-def _side_stream(device) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for work that overlaps
-    the expert GEMMs on torch's current stream."""
-    idx = torch.device(device).index
-    if idx is None:
-        idx = torch.cuda.current_device()
-    st = _SIDE_STREAMS.get(idx)
-    if st is None:
-        st = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
-    return st
-
-
 def _ws(nbytes: int, device) -> Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
@@ -755,27 +740,7 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     d_w = torch.empty(T, k, dtype=torch.float32, device=dev)
     call("moe_combine_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
          ptr(d_w), s, tag="combine_bwd")
-    # The routing weights' consumer (the router backward, a few small
-    # launches) runs on a side stream while the input-gradient GEMMs run on
-    # this one, and joins before the permute backward reads its result: the
-    # GEMMs hold every CU, and the small kernels fill the CUs their tails leave
-    # idle.  The side stream's tensors are marked as used by this one (and
-    # d_w as used by the side stream) for the caching allocator.
-    main = torch.cuda.current_stream(dev)
-    side = None
-    d_add = None
-    if on_d_weights is not None and _lib.TIMER.enabled and _lib.TIMER.only is None:
-        # a pass that times every launch by events: in order, so that each
-        # launch's events bracket that launch alone
-        d_add = on_d_weights(d_w)
-    elif on_d_weights is not None:
-        side = _side_stream(dev)
-        side.wait_stream(main)
-        d_w.record_stream(side)
-        with torch.cuda.stream(side):
-            d_add = on_d_weights(d_w)
-        if d_add is not None:
-            d_add.record_stream(main)
+    d_add = on_d_weights(d_w) if on_d_weights is not None else None
     d_pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
     call("moe_grouped_gemm_dgrad_swiglu_bwd", ptr(dy), ptr(down_proj), ptr(pre), ptr(offsets), E, S, H, I,
          ptr(d_pre), s, tag="down_dgrad")
@@ -787,8 +752,6 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     call("moe_grouped_gemm_dgrad", ptr(d_pre), ptr(gate_up_proj), ptr(offsets), E, S, 2 * I, H, ptr(d_xp), s,
          tag="up_dgrad")
     d_hidden = torch.empty(T, H, dtype=BF16, device=dev)
-    if side is not None:
-        main.wait_stream(side)
     call("moe_permute_bwd", ptr(d_xp), ptr(pos_of_slot), ptr(offsets), E, T, H, k, ptr(d_add), ptr(d_hidden), s,
          tag="permute_bwd")
     d_gu = wgrad("gate_up_proj", d_pre, xp, 2 * I, H)
@@ -980,7 +943,6 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
     E = gu.shape[0]
     S = xp.shape[0]
     grads = {}
-    main = torch.cuda.current_stream(x.device)
 
     def router_backward(d_w):
         # The routing weights' gradient from the experts plus any the scores
@@ -997,8 +959,6 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
         lg = logits.float() if ctx.bf16_logits else logits
         dx_router, grads["router"] = router_bwd_kernels(x, rw, lg, idx, d_logits, ds, ctx.norm, tw, stats, d_aux,
                                                         rw_target, bf16_logits=ctx.bf16_logits)
-        if grads["router"] is not None:  # made on the stream this runs on, used on the block's
-            grads["router"].record_stream(main)
         return dx_router
 
     params = {"gate_up_proj": (gu, targets[1]), "down_proj": (dn, targets[2])}
