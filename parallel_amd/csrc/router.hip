@@ -1287,14 +1287,14 @@ __global__ __launch_bounds__(kRbWaves * kWave) void router_bwd_gemm_kernel(
   const int grp = wave >> 2, rw = wave & 3;
   const int q = lane >> 4, i16 = lane & 15;
   // Block -> (column slice, token chunk).  Launch indices are dealt to the 8
-  // XCDs in turn; each XCD takes a run of consecutive column slices (all
-  // their chunks), so the two blocks writing the halves of a 128-byte dX line
-  // (HN 32) share an L2.
+  // XCDs in turn; each XCD takes a run of consecutive blocks in chunk-major
+  // order, so a token chunk's dZ rows are fetched into few L2s (one or two of
+  // the eight) and the two blocks reading or writing the halves of a 128-byte
+  // X or dX line (HN 32) share an L2.
   const int nb = gridDim.x;
   int b = blockIdx.x;
   if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
-  const int ns = nb / nh;
-  const int sp = b % ns, hb = b / ns;
+  const int sp = b / nh, hb = b % nh;
   const int h0 = hb * HN;
   const int tb = sp * tchunk, te = min(T, tb + tchunk);
   const int nit = (te - tb + 2 * kRbTok - 1) / (2 * kRbTok);  // iterations of two sub-steps
