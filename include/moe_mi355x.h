@@ -143,7 +143,9 @@ int moe_router_aux_bwd_bf16(const float* logits, const int64_t* indices,
 
 /* Backward of the router GEMM (F.linear, modeling_qwen3_moe.py:260) from
  * bf16 d_logits[T,E]: dx[T,H] = d_logits · wr (bf16) and dwr[E,H] =
- * d_logitsᵀ · x (bf16, reduced in f32 over row chunks held in the workspace).
+ * d_logitsᵀ · x (bf16, reduced in f32 over token chunks held in the
+ * workspace, always in chunk order; for E <= 128 a multiple of 32 and H a
+ * multiple of 32 one kernel forms dx and the chunks' partials together).
  * With dwr_accumulate, dwr holds an existing bf16 gradient and receives
  * bf16(dwr + bf16(d_logitsᵀ · x)), torch's accumulation of the fresh gradient
  * (parallel/parallel/engine/engine.py:165-178). */
