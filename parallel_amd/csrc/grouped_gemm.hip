@@ -226,6 +226,12 @@ __device__ __forceinline__ T* uniform_ptr(T* ptr) {
 __device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t off, uint4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{v.x, v.y, v.z, v.w}, rsrc, off, 0, 0);
 }
+// The same store marked non-temporal (cache policy nt): for outputs no kernel
+// of the step reads back (the weight gradients), so that their bytes do not
+// push the operands still being streamed out of L2 and the last-level cache.
+__device__ __forceinline__ void store16_nt(__amdgpu_buffer_rsrc_t rsrc, uint32_t off, uint4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{v.x, v.y, v.z, v.w}, rsrc, off, 0, 2);
+}
 __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -821,8 +827,13 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
               v.z += __uint_as_float(o.z);
               v.w += __uint_as_float(o.w);
             }
-            store16(rsC, off, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
-                                         __float_as_uint(v.w)));
+            const uint4 o4 = make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                        __float_as_uint(v.w));
+            if constexpr (EPI == EPI_WGRAD) {
+              store16_nt(rsC, off, o4);
+            } else {
+              store16(rsC, off, o4);
+            }
           }
       }
       return;
@@ -917,7 +928,7 @@ __global__ __launch_bounds__(CFG::kThreads) void grouped_gemm_kernel(const GemmP
               for (int e = 0; e < 8; ++e) a[e] += o[e];
               v = to_bf16x8(a);
             }
-            store16(rsC, out_off[n], v);
+            store16_nt(rsC, out_off[n], v);
           }
         }
       }
