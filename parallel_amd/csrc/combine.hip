@@ -101,7 +101,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_bwd_kernel(const bf16_t*
       if (d_scores) {
 #pragma unroll
         for (int j = 0; j < KM; ++j)
-          if (KT || j < k) v[j] = reinterpret_cast<const uint4*>(y + static_cast<int64_t>(sl.pos[j]) * H)[c];
+          if (KT || j < k)  // the backward's last read of the expert outputs
+            v[j] = ntload16(reinterpret_cast<const uint4*>(y + static_cast<int64_t>(sl.pos[j]) * H) + c);
       }
 #pragma unroll
       for (int j = 0; j < KM; ++j) {

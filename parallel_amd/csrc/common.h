@@ -20,6 +20,15 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
+// A 16-byte load marked non-temporal (cache policy nt), for the last read of
+// a tensor in the step by a kernel that reads each byte once: the caches then
+// keep what later kernels still read.
+typedef unsigned ntv4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ntload16(const void* p) {
+  const ntv4_t v = __builtin_nontemporal_load(reinterpret_cast<const ntv4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }

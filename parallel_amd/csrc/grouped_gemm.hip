@@ -1449,9 +1449,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(bf16_t* __restrict__ d_
     const unsigned r = c / cpr, k = (c - r * cpr) * 8;
     bf16_t* dr = d_pre + static_cast<size_t>(r) * 2 * I;
     const bf16_t* pr = pre + static_cast<size_t>(r) * 2 * I;
-    const uint4 dv = *reinterpret_cast<const uint4*>(dr + I + k);
-    const uint4 gv = *reinterpret_cast<const uint4*>(pr + k);
-    const uint4 uv = *reinterpret_cast<const uint4*>(pr + I + k);
+    const uint4 dv = ntload16(dr + I + k);  // the last reads of d_act and of the saved pre-activations
+    const uint4 gv = ntload16(pr + k);
+    const uint4 uv = ntload16(pr + I + k);
     const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
     uint32_t og[4], ou[4];
 #pragma unroll

@@ -264,7 +264,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_bwd_kernel(const bf16_t*
       uint4 v[KM];
 #pragma unroll
       for (int j = 0; j < KM; ++j)
-        if (KT || j < k) v[j] = reinterpret_cast<const uint4*>(dperm + static_cast<int64_t>(sl.pos[j]) * H)[c];
+        if (KT || j < k)  // the last read of the permuted rows' gradient
+          v[j] = ntload16(reinterpret_cast<const uint4*>(dperm + static_cast<int64_t>(sl.pos[j]) * H) + c);
       uint4 va = make_uint4(0, 0, 0, 0);
       if (d_add) va = reinterpret_cast<const uint4*>(d_add + static_cast<int64_t>(t) * H)[c];
       float acc[8];
