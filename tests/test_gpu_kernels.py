@@ -370,6 +370,68 @@ def test_grouped_gemm_wgrad(name, cnt, N, K, accumulate, f32):
             close_bf16(dw[e], ref, f"wgrad {name} g{e}", max_rel=8e-3)
 
 
+def _skewed_counts(name):
+    g = np.random.default_rng(len(name))
+    if name == "zipf200":  # one tile per group, Zipf rows, a tenth of the groups empty
+        c = (3000 / np.arange(1, 201) ** 1.1).astype(np.int64)
+        c[g.choice(200, 20, replace=False)] = 0
+        return g.permutation(c).tolist(), 256, 192
+    if name == "many1000":  # ten heavy groups among 990 of 0-20 rows: light XCD ranges touch > 64 groups
+        c = g.integers(0, 21, 1000)
+        c[g.choice(1000, 10, replace=False)] = g.integers(2000, 4001, 10)
+        return c.tolist(), 128, 320
+    if name == "ties64":  # 60 groups of equal cost between 4 heavy ones
+        c = np.full(64, 96)
+        c[[3, 17, 40, 63]] = 4000
+        return c.tolist(), 256, 256
+    return [1, 0, 5000, 2, 0, 33], 296, 264  # "ragged": ragged tiles on both sides
+
+
+@pytest.mark.parametrize("name,accumulate,f32", [("zipf200", 0, 0), ("many1000", 0, 0), ("many1000", 1, 0),
+                                                 ("ties64", 0, 0), ("ties64", 0, 1), ("ragged", 1, 1)])
+def test_grouped_gemm_wgrad_skewed_routing(name, accumulate, f32):
+    """Weight gradients under skewed row counts, where the tiles are split over
+    the XCDs by cost and dealt in cost order: many groups per XCD range (more
+    than 64 in the light ranges of many1000), groups of equal cost, ragged
+    tiles.  Every group against an fp32 product on the GPU."""
+    cnt, N, K = _skewed_counts(name)
+    counts, offs = _groups(cnt)
+    M, G = int(counts.sum()), len(cnt)
+    dc = torch.randn(M, N, generator=gen(8)).to(BF).to(DEV)
+    a = torch.randn(M, K, generator=gen(9)).to(BF).to(DEV)
+    odt = torch.float32 if f32 else BF
+    start = torch.randn(G, N, K, generator=gen(10)).to(odt).to(DEV)
+    dw = start.clone()
+    _lib.call("moe_grouped_gemm_wgrad", dc.data_ptr(), a.data_ptr(), (od := offs.to(DEV)).data_ptr(), G, M, N, K,
+              dw.data_ptr(), f32, accumulate, _lib.stream_of(dw))
+    ref = torch.zeros(G, N, K, device=DEV)
+    s = 0
+    for e, c in enumerate(cnt):
+        if c:
+            ref[e] = dc[s:s + c].float().t() @ a[s:s + c].float()
+        s += c
+    if accumulate:
+        ref += start.float()
+    live = counts.to(DEV) > 0
+    got = dw.float()
+    assert torch.isfinite(got).all()
+    scale = ref.abs().amax((1, 2)).clamp_min(1e-30)
+    rel = (got - ref).abs().amax((1, 2)) / scale
+    cos = F.cosine_similarity(got.reshape(G, -1).double(), ref.reshape(G, -1).double(), dim=1)
+    # bf16 output: one rounding of each element (2^-9 of it), two with the
+    # accumulate (the fresh sum's, then the sum with the old gradient's);
+    # fp32 output: the fp32 summation order alone.
+    bar = 1e-4 if f32 else (1.6e-2 if accumulate else 8e-3)
+    bad = live & ((rel > bar) | (cos < 0.9999))
+    assert not bad.any(), f"{name}: groups {bad.nonzero().flatten().tolist()[:8]} off (max rel {float(rel[live].max()):.3e})"
+    empty = ~live
+    if accumulate:
+        assert torch.equal(dw[empty], start[empty]), "accumulate must leave empty groups untouched"
+    else:
+        assert not dw[empty].any(), "empty groups must get zero gradients"
+    print(f"{name}: {G} groups, {M} rows, worst rel {float(rel[live].max()):.2e}")
+
+
 @pytest.mark.parametrize("cnt,I,H", [([256, 0, 300, 1, 128], 768, 2048), ([5, 64, 0, 17], 64, 96),
                                      ([600, 0, 1500, 5, 257], 768, 2048)])  # the last on the ping-pong loop
 def test_swiglu_fwd_and_fused_backward(cnt, I, H):
