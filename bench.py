@@ -55,6 +55,7 @@ def kernel_work(w, T: int, S: int):
     b = 4 if w.dtype == "fp32" else 2  # bytes per activation / weight element
     Wgu, Wdn = E * 2 * I * H * b, E * H * I * b  # expert weights
     xp, act, pre, y = S * H * b, S * I * b, S * 2 * I * b, S * H * b  # permuted rows, SwiGLU act, gate|up, down out
+    fused_router = 0.0 if (w.local_experts or w.dtype == "fp32") else 6.0 * T * E + 8.0 * T * k
     return {
         "up_fwd": (4.0 * S * H * I, xp + Wgu + act + pre),
         "down_fwd": (2.0 * S * H * I, act + Wdn + y),
@@ -67,7 +68,9 @@ def kernel_work(w, T: int, S: int):
         # read each x row once and the routes, write permuted rows and maps
         "permute_fwd": (None, T * H * b + S * H * b + 16.0 * S),
         "combine_fwd": (None, S * H * b + 8.0 * S + T * H * b),
-        "combine_bwd": (None, T * H * b + 2.0 * S * H * b + 12.0 * S),
+        # the bf16 block's combine backward also runs the router's top-k
+        # backward: logits and routes in, bf16 d_logits out
+        "combine_bwd": (None, T * H * b + 2.0 * S * H * b + 12.0 * S + fused_router),
         # the routes' rows, the router's dX added in (d_add), and d_hidden
         "permute_bwd": (None, S * H * b + 2.0 * T * H * b + 4.0 * S),
         # logits in, bf16 d_logits out (the aux gradient formed in the same pass)
@@ -110,6 +113,7 @@ _TAG_KERNELS = {
     "scatter_rows_kernel": "permute_fwd",
     "combine_fwd_kernel": "combine_fwd",
     "combine_bwd_kernel": "combine_bwd",
+    "combine_router_bwd_kernel": "combine_bwd",  # the block's combine backward with the router top-k backward
     "permute_bwd_kernel": "permute_bwd",
     "swiglu_bwd_kernel": "down_dgrad",
 }

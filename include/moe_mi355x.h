@@ -297,6 +297,28 @@ int moe_combine_bwd(const void* d_out, const void* y,
                     int64_t H, int64_t k, void* d_y, float* d_scores,
                     void* stream);
 
+/* moe_combine_bwd followed, token by token in the same launch, by the
+ * router's top-k backward on the routing weights' gradient it forms (the
+ * gradient of the router's scores in the one-op block, where nothing else
+ * uses them): d_logits_bf16[T,E] is what moe_router_topk_bwd_bf16
+ * (stats and d_aux NULL, bf16_terms 0), moe_router_aux_bwd_bf16 (bf16_terms
+ * 0) or moe_router_bf16_logits_bwd (bf16_terms 1) gives on that d_scores,
+ * bit for bit, with d_logits the incoming logits gradient (may be NULL);
+ * d_scores (may be NULL) receives the weights' gradient as moe_combine_bwd
+ * writes it.  logits fp32 [T,E], indices [T,k] int64 as the router wrote
+ * them.  Fuses the autograd of TF/integrations/moe.py:461-478 with that of
+ * TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267 (and :514-593 with
+ * stats/d_aux). */
+int moe_combine_router_bwd(const void* d_out, const void* y,
+                           const int32_t* pos_of_slot, const int32_t* offsets,
+                           int64_t num_buckets, const float* scores, int64_t T,
+                           int64_t H, int64_t k, void* d_y, float* d_scores,
+                           const float* logits, const int64_t* indices,
+                           const float* d_logits, const float* token_weight,
+                           const float* stats, const float* d_aux, int64_t E,
+                           int norm_topk_prob, int bf16_terms,
+                           void* d_logits_bf16, void* stream);
+
 /* ------------------------------------------------------------ grouped GEMM */
 /* Groups partition the rows of the activation operand: group g owns rows
  * [offs[g-1], offs[g]) (offs[-1] = 0; offs is the inclusive int32 cumsum,

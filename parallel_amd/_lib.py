@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "moe_combine_bwd": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "moe_combine_router_bwd": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _I64, _I, _I, _P, _P]),
     "moe_grouped_gemm_swiglu_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_grouped_gemm_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "moe_grouped_gemm_dgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),

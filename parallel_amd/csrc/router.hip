@@ -14,97 +14,9 @@
 
 #include "dma.h"
 #include "gemm.h"
+#include "router_token.h"
 
 namespace moe {
-
-constexpr int kMaxPerLane = 16;  // E <= 1024
-constexpr int kMaxTopK = 16;
-constexpr int kRouterWaves = 4;  // waves per block
-
-// Token layout.  A token occupies LPT consecutive lanes: one 16-lane DPP row
-// (E <= 256, four tokens per wave) or the whole wave (E <= 1024).  Lane `sub`
-// of a token holds experts sub, sub + LPT, ... (NPL of them, a power of two),
-// so the softmax statistics and the k-way selection are reductions over the
-// token's lanes with no LDS.  With 16-lane rows each reduction is 4 DPP steps
-// serving 4 tokens at once; one token per wave spent about 850 VALU
-// instructions per token, most of them in 6-step wave reductions.
-// The kernels are instantiated per (LPT, NPL) and KT (top-k; 0 = any k up to
-// kMaxTopK), so that the per-lane loops have fixed trip counts.  Items past E
-// read as -inf and are never selected; the arithmetic is that of any NPL
-// large enough for E.
-template <int LPT>
-struct Tok {
-  static_assert(LPT == 16 || LPT == kWave, "a token is one DPP row or one wave");
-  static constexpr int kPerBlock = kRouterWaves * (kWave / LPT);
-  __device__ static int sub() { return threadIdx.x & (LPT - 1); }
-  // The token's slot in the block (wave-major, then row).
-  __device__ static int slot() { return threadIdx.x / LPT; }
-};
-
-// Reductions over a token's lanes.  Every lane of the token gets the result,
-// bit for bit: each butterfly step combines a pair of lanes commutatively.
-template <int LPT>
-__device__ __forceinline__ float tok_max(float v) {
-  if constexpr (LPT == kWave) {
-    return wave_max(v);
-  } else {
-    v = fmaxf(v, dpp_move<dpp::kQuadXor1>(v, v));
-    v = fmaxf(v, dpp_move<dpp::kQuadXor2>(v, v));
-    v = fmaxf(v, dpp_move<dpp::kHalfMirror>(v, v));
-    return fmaxf(v, dpp_move<dpp::kMirror>(v, v));
-  }
-}
-template <int LPT>
-__device__ __forceinline__ float tok_sum(float v) {
-  if constexpr (LPT == kWave) {
-    return wave_sum(v);
-  } else {
-    v += dpp_move<dpp::kQuadXor1>(0.0f, v);
-    v += dpp_move<dpp::kQuadXor2>(0.0f, v);
-    v += dpp_move<dpp::kHalfMirror>(0.0f, v);
-    return v + dpp_move<dpp::kMirror>(0.0f, v);
-  }
-}
-template <int LPT>
-__device__ __forceinline__ void tok_argmax(float& v, int& i) {
-  if constexpr (LPT == kWave) {
-    wave_argmax(v, i);
-  } else {
-    argmax_step<dpp::kQuadXor1>(v, i);
-    argmax_step<dpp::kQuadXor2>(v, i);
-    argmax_step<dpp::kHalfMirror>(v, i);
-    argmax_step<dpp::kMirror>(v, i);
-  }
-}
-
-// Loads one token's logits; absent experts read as -inf.
-template <int LPT, int NPL>
-__device__ __forceinline__ void load_row(const float* row, int E, float (&v)[NPL]) {
-  const int sub = Tok<LPT>::sub();
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    const int e = sub + j * LPT;
-    v[j] = e < E ? row[e] : -INFINITY;
-  }
-}
-
-struct SoftmaxStats {
-  float max, sum;
-};
-
-template <int LPT, int NPL>
-__device__ __forceinline__ SoftmaxStats softmax_stats(const float (&v)[NPL]) {
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) m = fmaxf(m, v[j]);
-  m = tok_max<LPT>(m);
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    if (v[j] != -INFINITY) s += expf(v[j] - m);
-  s = tok_sum<LPT>(s);
-  return {m, s};
-}
 
 // k-way selection: sel_idx/sel_logit are the same in all lanes of the token.
 template <int LPT, int NPL, int KM>
@@ -564,119 +476,17 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     int E, int k_rt, int norm, const float* d_add, float* d_logits, bf16_t* __restrict__ d_logits_bf16,
     const float* __restrict__ token_weight, const float* __restrict__ aux_stats, const float* __restrict__ d_aux,
     int bf16_terms) {
-  constexpr int KM = KT ? KT : kMaxTopK;
+  using Row = TopkBwdRow<LPT, NPL, KT>;
   const int k = KT ? KT : k_rt;
-  const int sub = Tok<LPT>::sub();
   const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
   if (t >= T) return;
-  float v[NPL];
-  const float* row = logits + static_cast<int64_t>(t) * E;
-  const int64_t base = static_cast<int64_t>(t) * E;
-  load_row<LPT>(row, E, v);
-  // The added gradient is loaded with the logits, not after the arithmetic.
-  float add[NPL];
+  Row row;
+  topk_bwd_load(row, logits, indices, d_add, t, E, k, token_weight, aux_stats, d_aux);
+  float ds[Row::KM];
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    const int e = sub + j * LPT;
-    add[j] = (d_add && e < E) ? d_add[base + e] : 0.0f;
-  }
-  const SoftmaxStats st = softmax_stats<LPT>(v);
-  const float inv_sum = 1.0f / st.sum;
-  auto round_bf16 = [](float x) { return bf16_to_f32(f32_to_bf16(x)); };
-  if (aux_stats) {
-    // aux_bwd_kernel's term: p_e (g_e - <g, p>), g_e = d_aux E w c_e / W^2.
-    const float W = aux_stats[E];
-    const float w = token_weight ? token_weight[t] : 1.0f;
-    const float scale = d_aux[0] * static_cast<float>(E) * w / (W * W);
-    float p[NPL], g[NPL];
-    float dot = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const int e = sub + j * LPT;
-      p[j] = 0.0f;
-      g[j] = 0.0f;
-      if (e < E) {
-        p[j] = expf(v[j] - st.max) * inv_sum;
-        g[j] = scale * aux_stats[e];
-        dot += p[j] * g[j];
-      }
-    }
-    dot = tok_sum<LPT>(dot);
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const float d = p[j] * (g[j] - dot);
-      if (bf16_terms) {
-        add[j] = d_add ? round_bf16(add[j] + round_bf16(d)) : round_bf16(d);
-      } else {
-        add[j] = d_add ? add[j] + d : d;
-      }
-    }
-  }
-
-  int idx[KM];
-  float pv[KM], ds[KM];
-  float tot = 0.0f;
-#pragma unroll
-  for (int r = 0; r < KM; ++r) {
-    if (r < k) {
-      int64_t id = indices[static_cast<int64_t>(t) * k + r];
-      bool ok = id >= 0 && id < E;
-      idx[r] = ok ? static_cast<int>(id) : -1;
-      ds[r] = d_scores[static_cast<int64_t>(t) * k + r];
-      // bf16 logits come with bf16 scores, whose gradient is a bf16 tensor
-      if (bf16_terms) ds[r] = round_bf16(ds[r]);
-      float lv;
-      if constexpr (LPT == kWave) {
-        // One token per wave: the selected logit is already in lane e % 64
-        // (v[e / 64]), fetched by readlane rather than a second load.
-        const int e = __builtin_amdgcn_readfirstlane(ok ? idx[r] : 0);
-        float cand = v[0];
-#pragma unroll
-        for (int j = 1; j < NPL; ++j) cand = (e / kWave == j) ? v[j] : cand;
-        lv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), e & (kWave - 1)));
-      } else {
-        lv = ok ? row[idx[r]] : 0.0f;
-      }
-      pv[r] = ok ? expf(lv - st.max) * inv_sum : 0.0f;
-      tot += pv[r];
-    }
-  }
-  // Renormalisation backward: s_r = v_r / V  ->  dv_r = (ds_r - sum_i ds_i s_i) / V.
-  float dv[KM];
-  if (norm) {
-    float dot = 0.0f;
-#pragma unroll
-    for (int r = 0; r < KM; ++r)
-      if (r < k) dot += ds[r] * (pv[r] / tot);
-#pragma unroll
-    for (int r = 0; r < KM; ++r)
-      if (r < k) dv[r] = (ds[r] - dot) / tot;
-  } else {
-#pragma unroll
-    for (int r = 0; r < KM; ++r)
-      if (r < k) dv[r] = ds[r];
-  }
-  float c = 0.0f;  // <dp, p> = sum_r dv_r p_{idx_r}
-#pragma unroll
-  for (int r = 0; r < KM; ++r)
-    if (r < k) c += dv[r] * pv[r];
-
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    const int e = sub + j * LPT;
-    if (e < E) {
-      float dp = 0.0f;
-#pragma unroll
-      for (int r = 0; r < KM; ++r)
-        if (r < k && idx[r] == e) dp += dv[r];
-      float p = expf(v[j] - st.max) * inv_sum;
-      float g = p * (dp - c);
-      if (bf16_terms) g = round_bf16(g);
-      if (d_add || aux_stats) g += add[j];
-      if (d_logits) d_logits[base + e] = g;
-      if (d_logits_bf16) d_logits_bf16[base + e] = f32_to_bf16(g);
-    }
-  }
+  for (int q = 0; q < Row::KM; ++q) ds[q] = q < k ? d_scores[static_cast<int64_t>(t) * k + q] : 0.0f;
+  topk_bwd_finish(row, ds, logits, t, E, k, norm, d_add != nullptr, aux_stats != nullptr, d_logits, d_logits_bf16,
+                  bf16_terms);
 }
 
 // ------------------------------------------------------------------ aux loss
@@ -853,44 +663,6 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void aux_bwd_kernel(const flo
 using namespace moe;
 
 namespace {
-// Instantiation for E experts: lanes per token, experts per lane rounded up
-// to a power of two, and top-k k (the specialised k, or the generic 0).  The
-// selecting kernels take 16 lanes per token up to 256 experts (their k rounds
-// of reductions dominate); the backward kernels, which only stream a row in
-// and out, keep one wave per token so that more waves hide their loads.
-template <bool kWaveToken = false, class F>
-void with_npl(int64_t E, F&& f) {
-  using L16 = std::integral_constant<int, 16>;
-  using L64 = std::integral_constant<int, kWave>;
-  static_assert(16 * kMaxPerLane == 256, "E <= 256 fits 16 lanes per token");
-  if (!kWaveToken && E <= 256) {
-    if (E <= 16) f(L16{}, std::integral_constant<int, 1>{});
-    else if (E <= 32) f(L16{}, std::integral_constant<int, 2>{});
-    else if (E <= 64) f(L16{}, std::integral_constant<int, 4>{});
-    else if (E <= 128) f(L16{}, std::integral_constant<int, 8>{});
-    else f(L16{}, std::integral_constant<int, 16>{});
-  } else {
-    if (E <= 64) f(L64{}, std::integral_constant<int, 1>{});
-    else if (E <= 128) f(L64{}, std::integral_constant<int, 2>{});
-    else if (E <= 256) f(L64{}, std::integral_constant<int, 4>{});
-    else if (E <= 512) f(L64{}, std::integral_constant<int, 8>{});
-    else f(L64{}, std::integral_constant<int, 16>{});
-  }
-}
-template <bool kWaveToken = false, class F>
-void with_npl_k(int64_t E, int64_t k, F&& f) {
-  with_npl<kWaveToken>(E, [&](auto L, auto N) {
-    switch (k) {
-      case 1: f(L, N, std::integral_constant<int, 1>{}); break;
-      case 2: f(L, N, std::integral_constant<int, 2>{}); break;
-      case 4: f(L, N, std::integral_constant<int, 4>{}); break;
-      case 6: f(L, N, std::integral_constant<int, 6>{}); break;
-      case 8: f(L, N, std::integral_constant<int, 8>{}); break;
-      default: f(L, N, std::integral_constant<int, 0>{}); break;
-    }
-  });
-}
-
 // Blocks covering T tokens.
 int token_blocks(int64_t T, int64_t E, bool wave_token = false) {
   const int64_t tpb = wave_token ? kRouterWaves : tokens_per_block(E);

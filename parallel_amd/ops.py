@@ -221,11 +221,20 @@ def router_bwd_kernels(x: Tensor, weight: Tensor, logits: Tensor, indices: Tenso
     else:
         call("moe_router_topk_bwd_bf16", ptr(logits), ptr(indices), ptr(d_scores), ptr(d_add), T, E, k,
              int(norm_topk_prob), ptr(dl_bf16), s, tag="router_topk_bwd")
+    return _router_gemm_bwd(x, weight, dl_bf16, dw_target)
+
+
+def _router_gemm_bwd(x: Tensor, weight: Tensor, dl_bf16: Tensor,
+                     dw_target: Tensor | None) -> tuple[Tensor, Tensor | None]:
+    """The router linear's backward from the bf16 logits gradient: (dx [T,H]
+    bf16, dweight [E,H], or None when added into ``dw_target``)."""
+    T, H = x.shape
+    E = weight.shape[0]
     dx = torch.empty(T, H, dtype=BF16, device=x.device)
     dw = dw_target if dw_target is not None else torch.empty(E, H, dtype=weight.dtype, device=x.device)
     ws = _ws(_lib.load().moe_router_logits_bwd_workspace_bytes(T, H, E), x.device)
     call("moe_router_logits_bwd", ptr(dl_bf16), ptr(x), ptr(weight), ptr(dx), ptr(dw), int(dw_target is not None),
-         T, H, E, ptr(ws), ws.numel(), s, tag="router_gemm_bwd")
+         T, H, E, ptr(ws), ws.numel(), _stream(x), tag="router_gemm_bwd")
     return dx, (None if dw_target is not None else dw)
 
 
@@ -717,13 +726,20 @@ def _(hidden, top_k_index, top_k_weights, gate_up_proj, down_proj, accumulate_gr
 
 def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor, down_proj: Tensor, xp: Tensor,
                         pre: Tensor, act: Tensor, y: Tensor, pos_of_slot: Tensor, offsets: Tensor,
-                        wgrad, on_d_weights=None) -> tuple[Tensor, Tensor, object, object]:
+                        wgrad, on_d_weights=None, router: dict | None = None) -> tuple[Tensor, Tensor | None, object,
+                                                                                        object]:
     """The expert backward's launches; ``wgrad(name, dc, a, n, k)`` issues the
     weight gradient dW[g][n,k] = dc[rows of g]ᵀ · a[rows of g] of projection
     ``name`` ("gate_up_proj", then "down_proj") and returns whatever stands for
     it.  ``on_d_weights(d_weights)``, if given, runs as soon as the routing
     weights' gradient exists and returns a bf16 [T,H] gradient that the
     permute backward adds into d_hidden (the other path to the same input).
+    With ``router`` (bf16 rows only; the routing weights are the router's
+    scores and nothing else uses them) the combine backward also runs the
+    router's top-k backward on the weights' gradient in the same launch
+    (moe_combine_router_bwd, the bits of the two separate launches), and
+    ``router["finish"](d_logits_bf16)`` returns the bf16 [T,H] gradient the
+    permute backward adds; d_weights is then not formed (None).
     Returns (d_hidden [T,H], d_weights [T,k] f32, wgrad's two results)."""
     if xp.dtype == torch.float32:
         return _experts_bwd_f32(d_out, top_k_weights.float().contiguous(), gate_up_proj, down_proj, xp, pre, act, y,
@@ -737,10 +753,21 @@ def experts_bwd_kernels(d_out: Tensor, top_k_weights: Tensor, gate_up_proj: Tens
     d_out = d_out.to(BF16).contiguous()
     w = top_k_weights.float().contiguous()
     dy = torch.empty(S, H, dtype=BF16, device=dev)
-    d_w = torch.empty(T, k, dtype=torch.float32, device=dev)
-    call("moe_combine_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
-         ptr(d_w), s, tag="combine_bwd")
-    d_add = on_d_weights(d_w) if on_d_weights is not None else None
+    if router is not None:
+        d_w = None
+        lg = router["logits"]
+        n_e = lg.shape[1]
+        dl_bf16 = torch.empty(T, n_e, dtype=BF16, device=dev)
+        call("moe_combine_router_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
+             None, ptr(lg), ptr(router["indices"]), ptr(router["d_logits"]), ptr(router["token_weight"]),
+             ptr(router["stats"]), ptr(router["d_aux"]), n_e, int(router["norm"]), int(router["bf16_terms"]),
+             ptr(dl_bf16), s, tag="combine_bwd")
+        d_add = router["finish"](dl_bf16)
+    else:
+        d_w = torch.empty(T, k, dtype=torch.float32, device=dev)
+        call("moe_combine_bwd", ptr(d_out), ptr(y), ptr(pos_of_slot), ptr(offsets), E, ptr(w), T, H, k, ptr(dy),
+             ptr(d_w), s, tag="combine_bwd")
+        d_add = on_d_weights(d_w) if on_d_weights is not None else None
     d_pre = torch.empty(S, 2 * I, dtype=BF16, device=dev)
     call("moe_grouped_gemm_dgrad_swiglu_bwd", ptr(dy), ptr(down_proj), ptr(pre), ptr(offsets), E, S, H, I,
          ptr(d_pre), s, tag="down_dgrad")
@@ -975,8 +1002,24 @@ def _block_backward(ctx, d_out, d_logits, d_scores, _d_idx, d_aux, *_unused):
 
     if d_out is None:
         d_out = torch.zeros_like(x)
+    router = None
+    if d_scores is None and xp.dtype == BF16 and not (x.dtype == rw.dtype == torch.float32):
+        # Nothing but the experts uses the scores: the top-k backward runs
+        # inside the combine backward, on the weights' gradient it forms.
+        def finish(dl_bf16):
+            dx_router, grads["router"] = _router_gemm_bwd(x.contiguous(), rw.contiguous(), dl_bf16, rw_target)
+            return dx_router
+
+        with_aux = d_aux is not None
+        router = dict(logits=(logits.float() if ctx.bf16_logits else logits).contiguous(), indices=idx.contiguous(),
+                      d_logits=None if d_logits is None else d_logits.float().contiguous(),
+                      token_weight=tw.float().contiguous() if (with_aux and tw is not None) else None,
+                      stats=stats if with_aux else None,
+                      d_aux=d_aux.float().reshape(1).contiguous() if with_aux else None,
+                      norm=ctx.norm, bf16_terms=ctx.bf16_logits, finish=finish)
     dx, _d_w, d_gu, d_dn = experts_bwd_kernels(d_out, scores, gu, dn, xp, pre, act, y, pos, offsets, wgrad,
-                                              on_d_weights=router_backward)
+                                              on_d_weights=None if router is not None else router_backward,
+                                              router=router)
     return dx.to(ctx.x_dtype), grads["router"], d_gu, d_dn, None, None, None, None, None, None
 
 

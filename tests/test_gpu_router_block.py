@@ -320,3 +320,74 @@ def test_moe_block_bf16_logits_c2_routes_bit_exactly_and_matches_the_separate_op
     for name, ga, gb in zip(("dx", "d_router", "d_gate_up", "d_down"), a, b):
         close_bf16(ga.grad, gb.grad, f"c2 bf16-logit block {name}")
     assert torch.equal(a[2].grad, b[2].grad) and torch.equal(a[3].grad, b[3].grad)
+
+
+# T, H, E, k, norm, aux (with a token mask), incoming logits gradient, bf16
+# logits, share of sentinel slots.  E spans the experts-per-lane widths of
+# the one-wave-per-token backward (1, 2, 4, 16 per lane) and k the
+# specialised and run-time slot counts.
+COMBINE_ROUTER_CASES = [(4096, 2048, 128, 8, True, False, False, False, 0.0),
+                        (1000, 256, 64, 6, False, True, True, False, 0.05),
+                        (512, 128, 200, 4, True, True, True, True, 0.0),
+                        (300, 96, 32, 3, True, False, True, False, 0.1),
+                        (64, 64, 1000, 16, True, True, False, True, 0.0),
+                        (33, 72, 8, 1, False, False, False, False, 0.0)]
+
+
+@pytest.mark.parametrize("T,H,E,k,norm,aux,d_logits,bf16,sentinel", COMBINE_ROUTER_CASES)
+def test_combine_router_bwd_is_the_two_launches_bit_for_bit(T, H, E, k, norm, aux, d_logits, bf16, sentinel):
+    """moe_combine_router_bwd (the combine backward and the router's top-k
+    backward in one launch, as ops.moe_block runs them) against
+    moe_combine_bwd followed by the router top-k backward entry point on its
+    d_scores: d_y, d_scores and the bf16 logits gradient, bit for bit."""
+    from parallel_amd import _lib
+
+    g = gen(T + E + k)
+    I = 64
+    x = torch.randn(T, H, generator=g).to(BF).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.05).to(BF).to(DEV)
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(BF).to(DEV)
+    dn = (torch.randn(E, H, I, generator=g) * 0.05).to(BF).to(DEV)
+    tw = (torch.rand(T, generator=g) > 0.2).float().to(DEV) if aux else None
+    logits, scores, idx, _, stats = ops.router_aux_fwd(x, wr, k, norm, tw)
+    if bf16:
+        logits = logits.to(BF).float()  # the values of bf16 logits
+    ids = idx.clone()
+    if sentinel:
+        ids[(torch.rand(T, k, generator=g) < sentinel).to(DEV)] = E  # slots without an expert
+    _, _, _, _, y, pos, offsets = ops._experts_fwd_kernels(x, ids, scores, gu, dn)
+    d_out = torch.randn(T, H, generator=g).to(BF).to(DEV)
+    dl_in = (torch.randn(T, E, generator=g) * 0.01).to(DEV) if d_logits else None
+    d_aux = torch.tensor([0.7], device=DEV) if aux else None
+    st = stats if aux else None
+    S = T * k
+    s = _lib.stream_of(x)
+    dy1 = torch.empty(S, H, dtype=BF, device=DEV)
+    dw1 = torch.empty(T, k, device=DEV)
+    dl1 = torch.empty(T, E, dtype=BF, device=DEV)
+    _lib.call("moe_combine_bwd", _lib.ptr(d_out), _lib.ptr(y), _lib.ptr(pos), _lib.ptr(offsets), E,
+              _lib.ptr(scores), T, H, k, _lib.ptr(dy1), _lib.ptr(dw1), s)
+    if bf16:
+        _lib.call("moe_router_bf16_logits_bwd", _lib.ptr(logits), _lib.ptr(ids), _lib.ptr(dw1), _lib.ptr(dl_in),
+                  _lib.ptr(tw), _lib.ptr(st), _lib.ptr(d_aux), T, E, k, int(norm), _lib.ptr(dl1), s)
+    elif aux:
+        _lib.call("moe_router_aux_bwd_bf16", _lib.ptr(logits), _lib.ptr(ids), _lib.ptr(dw1), _lib.ptr(dl_in),
+                  _lib.ptr(tw), _lib.ptr(st), _lib.ptr(d_aux), T, E, k, int(norm), _lib.ptr(dl1), s)
+    else:
+        _lib.call("moe_router_topk_bwd_bf16", _lib.ptr(logits), _lib.ptr(ids), _lib.ptr(dw1), _lib.ptr(dl_in), T, E,
+                  k, int(norm), _lib.ptr(dl1), s)
+    for with_scores in (True, False):
+        dy2 = torch.full((S, H), float("nan"), dtype=BF, device=DEV)
+        dw2 = torch.full((T, k), float("nan"), device=DEV)
+        dl2 = torch.full((T, E), float("nan"), dtype=BF, device=DEV)
+        _lib.call("moe_combine_router_bwd", _lib.ptr(d_out), _lib.ptr(y), _lib.ptr(pos), _lib.ptr(offsets), E,
+                  _lib.ptr(scores), T, H, k, _lib.ptr(dy2), _lib.ptr(dw2) if with_scores else None, _lib.ptr(logits),
+                  _lib.ptr(ids), _lib.ptr(dl_in), _lib.ptr(tw), _lib.ptr(st), _lib.ptr(d_aux), E, int(norm),
+                  int(bf16), _lib.ptr(dl2), s)
+        torch.cuda.synchronize()
+        assert torch.equal(dy2, dy1), "d_y"
+        assert torch.equal(dl2, dl1), "d_logits"
+        if with_scores:
+            assert torch.equal(dw2, dw1), "d_scores"
+        else:
+            assert torch.isnan(dw2).all(), "d_scores written although not asked for"
