@@ -136,13 +136,14 @@ def test_bench_tags_kernel_dispatches_by_entry_point():
         g.format(0, "true", 1, small), "void moe::router_reduce_topk_kernel<2, 8>(float const*)",
         g.format(0, "true", 2, big), g.format(0, "true", 0, big), "void moe::combine_fwd_kernel<8>(unsigned short const*)",
         "void moe::combine_bwd_kernel<8>(unsigned short const*)",
+        "void moe::combine_router_bwd_kernel<8, 2>(unsigned short const*)",
         g.format(0, "false", 0, tall), "moe::swiglu_bwd_kernel(unsigned short*)", g.format(0, "false", 0, big),
         "void moe::permute_bwd_kernel<8>(unsigned short const*)", g.format(1, "false", 4, big),
         g.format(1, "false", 4, big),
         g.format(1, "false", 4, small), g.format(0, "false", 0, small),
     ]
     assert bench.tag_dispatches(names) == [
-        "router_fwd", "router_fwd", "up_fwd", "down_fwd", "combine_fwd", "combine_bwd",
+        "router_fwd", "router_fwd", "up_fwd", "down_fwd", "combine_fwd", "combine_bwd", "combine_bwd",
         "down_dgrad", "down_dgrad", "up_dgrad", "permute_bwd", "up_wgrad", "down_wgrad",
         "router_gemm_bwd", "router_gemm_bwd",
     ]
@@ -184,10 +185,23 @@ def test_zero_size_calls_accept_null_buffers_without_a_gpu():
         "topk_bwd_bf16": lambda: lib.moe_router_topk_bwd_bf16(None, None, None, None, 0, E, k, 1, None, None),
         "combine_fwd": lambda: lib.moe_combine_fwd(None, None, None, E, None, 0, H, k, None, None),
         "combine_bwd": lambda: lib.moe_combine_bwd(None, None, None, None, E, None, 0, H, k, None, None, None),
+        "combine_router_bwd": lambda: lib.moe_combine_router_bwd(None, None, None, None, E, None, 0, H, k, None, None,
+                                                                 None, None, None, None, None, None, E, 1, 0, None,
+                                                                 None),
         "permute_bwd": lambda: lib.moe_permute_bwd(None, None, None, E, 0, H, k, None, None, None),
     }
     for name, call in calls.items():
         assert call() == _lib.MOE_OK, f"{name}: {lib.moe_last_error()}"
+    # the fused combine + router top-k backward checks the router's sizes and arguments too
+    assert lib.moe_combine_router_bwd(b, b, b, b, E, None, 4, H, k, b, None, b, b, None, None, None, None, 2000, 1, 0,
+                                      b, None) == _lib.MOE_ERR_UNSUPPORTED
+    assert lib.moe_combine_router_bwd(b, b, b, b, E, None, 4, H, 8, b, None, b, b, None, None, None, None, 4, 1, 0,
+                                      b, None) == _lib.MOE_ERR_UNSUPPORTED
+    assert lib.moe_combine_router_bwd(b, b, b, b, E, None, 4, H, k, b, None, b, b, None, None, b, None, E, 1, 0,
+                                      b, None) == _lib.MOE_ERR_INVALID
+    assert b"stats and d_aux" in lib.moe_last_error()
+    assert lib.moe_combine_router_bwd(b, None, b, b, E, None, 4, H, k, b, None, b, b, None, None, None, None, E, 1, 0,
+                                      b, None) == _lib.MOE_ERR_INVALID
     # a missing non-empty operand is still an error
     assert lib.moe_grouped_gemm_fwd(None, None, b, E, 0, H, I, None, None) == _lib.MOE_ERR_INVALID
     assert lib.moe_grouped_gemm_fwd(None, b, b, E, 8, H, I, None, None) == _lib.MOE_ERR_INVALID
