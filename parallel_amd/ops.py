@@ -1045,7 +1045,9 @@ def moe_block(x: Tensor, router_weight: Tensor, gate_up_proj: Tensor, down_proj:
     loss of :514-593), but the backward adds the router's input gradient to
     the experts' inside the permute backward (one rounding of the sum of
     both in fp32, where autograd rounds the experts' sum, then adds), forms
-    the aux loss's logits gradient inside the top-k backward, and with
+    the aux loss's logits gradient inside the top-k backward (which runs
+    inside the combine backward when nothing else takes the scores'
+    gradient: the same bits as the separate launch), and with
     ``accumulate_grad`` adds every weight gradient into an existing ``.grad``
     (bf16 router weight; bf16 or fp32 expert weights) in the kernels, as
     ``experts`` does for the expert weights (with the same limits: no grad
