@@ -259,12 +259,15 @@ int moe_permute_fwd_noalloc(const void* hidden, int64_t T, int64_t H,
                             int32_t* pos_of_slot, int32_t* counts,
                             int32_t* offsets, void* stream);
 
-/* Per sorted position: local_ids[pos] = ids[perm[pos]] - bucket*divisor and
- * routed_scores[pos] = scores[perm[pos]] (either output may be NULL).
- * Replaces send_experts/send_scores of token_dispatch.py:124-125. */
+/* Per sorted position: local_ids[pos] = ids[perm[pos]] - bucket*divisor,
+ * routed_scores[pos] = scores[perm[pos]] and source_tokens[pos] =
+ * perm[pos] / k, the token of the slot (any output may be NULL).  Replaces
+ * send_experts/send_scores of token_dispatch.py:124-125 and the sorted
+ * source_tokens of :106-118. */
 int moe_dispatch_meta(const int64_t* ids, const float* scores,
                       const int32_t* perm, int64_t S, int64_t divisor,
-                      int64_t* local_ids, float* routed_scores, void* stream);
+                      int64_t k, int64_t* local_ids, float* routed_scores,
+                      int64_t* source_tokens, void* stream);
 
 /* Backward of the row gather: d_hidden[t,:] = sum_j d_permuted[pos_of_slot[t*k+j],:]
  * over valid positions (pos < offsets[nb-1]), fp32 accumulation, plus

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
 # MOE_MI355X_LIB selects another build of the same library (A/B comparisons).
 LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB") or Path(__file__).resolve().parent / "lib" / "libmoe_mi355x.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MOE_OK = 0
 MOE_ERR_INVALID = -1
@@ -58,7 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_f32_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "moe_f32_combine_bwd": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "moe_f32_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
-    "moe_dispatch_meta": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P]),
+    "moe_dispatch_meta": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "moe_permute_bwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "moe_combine_fwd": (_I, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "moe_combine_bwd": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),

@@ -75,4 +75,4 @@ int cached_blocks_per_cu(int dev, const void* kernel, int threads, int lds_bytes
 
 extern "C" const char* moe_last_error(void) { return moe::g_last_error; }
 
-extern "C" int moe_abi_version(void) { return 3; }
+extern "C" int moe_abi_version(void) { return 4; }

@@ -229,10 +229,12 @@ __global__ __launch_bounds__(kPermThreads) void scatter_rows_kernel(const bf16_t
 }
 
 __global__ void dispatch_meta_kernel(const int64_t* __restrict__ ids, const float* __restrict__ scores,
-                                     const int32_t* __restrict__ perm, int S, int64_t divisor,
-                                     int64_t* __restrict__ local_ids, float* __restrict__ routed_scores) {
+                                     const int32_t* __restrict__ perm, int S, int64_t divisor, int k,
+                                     int64_t* __restrict__ local_ids, float* __restrict__ routed_scores,
+                                     int64_t* __restrict__ source_tokens) {
   for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < S; pos += gridDim.x * blockDim.x) {
     int s = perm[pos];
+    if (source_tokens) source_tokens[pos] = s / k;  // slot s = t k + j of token t (s >= 0)
     if (local_ids) {
       // id - floor(id / divisor) * divisor (the reference's send_experts), in [0, divisor)
       const int64_t id = ids[s];
@@ -364,14 +366,16 @@ int permute_fwd_run(const void* hidden, int64_t T, int64_t H, const int64_t* ids
 }  // namespace moe
 
 extern "C" int moe_dispatch_meta(const int64_t* ids, const float* scores, const int32_t* perm, int64_t S,
-                                 int64_t divisor, int64_t* local_ids, float* routed_scores, void* stream) {
-  MOE_REQUIRE(S >= 0 && S < (1ll << 31) && divisor >= 1, MOE_ERR_INVALID, "dispatch meta: bad sizes");
+                                 int64_t divisor, int64_t k, int64_t* local_ids, float* routed_scores,
+                                 int64_t* source_tokens, void* stream) {
+  MOE_REQUIRE(S >= 0 && S < (1ll << 31) && divisor >= 1 && k >= 1 && k < (1ll << 31), MOE_ERR_INVALID,
+              "dispatch meta: bad sizes");
   if (S == 0) return MOE_OK;
   MOE_REQUIRE(ids && perm && (!routed_scores || scores), MOE_ERR_INVALID, "dispatch meta: null pointer");
   int blocks = static_cast<int>((S + 255) / 256);
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(dispatch_meta_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), ids, scores, perm,
-                     static_cast<int>(S), divisor, local_ids, routed_scores);
+                     static_cast<int>(S), divisor, static_cast<int>(k), local_ids, routed_scores, source_tokens);
   return launch_status("moe_dispatch_meta");
 }
 

@@ -1090,8 +1090,9 @@ def dispatch_fwd(hidden: Tensor, global_indices: Tensor, scores: Tensor, local_c
          ptr(pos), ptr(counts), ptr(offsets), ptr(ws), ws.numel(), s)
     send_experts = torch.empty(S, dtype=torch.int64, device=dev)
     send_scores = torch.empty(S, dtype=torch.float32, device=dev)
-    call("moe_dispatch_meta", ptr(ids), ptr(sc), ptr(perm), S, local_count, ptr(send_experts), ptr(send_scores), s)
-    source_tokens = torch.div(perm, k, rounding_mode="floor").to(torch.int64)
+    source_tokens = torch.empty(S, dtype=torch.int64, device=dev)
+    call("moe_dispatch_meta", ptr(ids), ptr(sc), ptr(perm), S, local_count, k, ptr(send_experts), ptr(send_scores),
+         ptr(source_tokens), s)
     return send_hidden, send_experts, send_scores.to(scores.dtype), source_tokens, pos, counts
 
 

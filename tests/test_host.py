@@ -189,6 +189,7 @@ def test_zero_size_calls_accept_null_buffers_without_a_gpu():
                                                                  None, None, None, None, None, None, E, 1, 0, None,
                                                                  None),
         "permute_bwd": lambda: lib.moe_permute_bwd(None, None, None, E, 0, H, k, None, None, None),
+        "dispatch_meta": lambda: lib.moe_dispatch_meta(None, None, None, 0, 4, k, None, None, None, None),
     }
     for name, call in calls.items():
         assert call() == _lib.MOE_OK, f"{name}: {lib.moe_last_error()}"
