@@ -112,6 +112,38 @@ def test_moe_block_matches_the_separate_ops_and_the_oracle(base, tokens):
     close_bf16(blk["dx"], sep["dx"], f"{base} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
 
 
+@pytest.mark.parametrize("base,tokens", [("c2", 512), ("c4", 1024)])
+def test_moe_block_with_score_and_logit_gradients_matches_the_separate_ops(base, tokens):
+    """When the scores and logits returned by moe_block also feed the loss,
+    the block's backward sums the scores' two gradients before the router's
+    top-k backward (the separate-launch path, not the combine's fused one)
+    and adds the logits' gradient there: the router weight's gradient is the
+    separate ops' bits, the expert weights' too."""
+    w = scaled(WORKLOADS[base], tokens)
+    inp = make_block_inputs(w, seed=12, dtype=BF)
+    bias = inp.get("logit_bias")
+    bias = None if bias is None else bias.to(DEV)
+    T, k, E = w.tokens, w.top_k, w.experts
+    d_scores = torch.randn(T, k, generator=gen(21)).to(DEV)
+    d_logits = (torch.randn(T, E, generator=gen(22)) * 0.01).to(DEV)
+    coef = torch.tensor(w.aux_coef, device=DEV)
+    d_out = inp["d_out"].to(DEV)
+    res = []
+    for fused_op in (True, False):
+        a = [inp[n].to(DEV).clone().requires_grad_() for n in ("x", "router_weight", "gate_up_proj", "down_proj")]
+        if fused_op:
+            out, logits, scores, _, aux = ops.moe_block(*a, k, w.norm_topk_prob, None, bias)
+        else:
+            logits, scores, idx, aux, _ = ops.router_aux_fwd(a[0], a[1], k, w.norm_topk_prob, None, bias)
+            out = ops.experts(a[0], idx, scores, a[2], a[3])
+        torch.autograd.backward([out, aux, scores, logits], [d_out, coef, d_scores, d_logits])
+        res.append([t.grad for t in a])
+    torch.cuda.synchronize()
+    (dx1, dr1, dg1, dd1), (dx2, dr2, dg2, dd2) = res
+    assert torch.equal(dr1, dr2) and torch.equal(dg1, dg2) and torch.equal(dd1, dd2)
+    close_bf16(dx1, dx2, f"{base} dx against the separate ops", max_rel=1e-2, min_cos=0.99999)
+
+
 @pytest.mark.parametrize("name", ["c2", "c4", "c5"])
 def test_moe_block_matches_the_separate_ops_at_full_size(name):
     """The benchmark configurations at full size (C4 with its biased router,
