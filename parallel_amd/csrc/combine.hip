@@ -4,7 +4,8 @@
 // step: the k expert rows of a token are read, scaled and summed in fp32 and
 // written once.  No atomics, so the result is deterministic; the backward
 // reads each token's output gradient once and produces both the row gradients
-// and the routing-score gradients (a wave dot product per routed slot).
+// and the routing-score gradients (a wave dot product per routed slot); its
+// fused form then runs the router's top-k backward on those gradients.
 //
 // Reference: TF/integrations/moe.py:461-478 (weight, mask, inverse permute,
 // sum over k in fp32) and parallel/parallel/engine/model_parallel/
