@@ -174,7 +174,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_router_bwd_kernel(
   static_assert(Row::KM == Slots<KT>::KM, "one score gradient per slot");
   const int lane = threadIdx.x & (kWave - 1);
   const int n_valid = *n_valid_ptr;
-  for (int t = blockIdx.x * kCombWaves + (threadIdx.x >> 6); t < T; t += gridDim.x * kCombWaves) {
+  for (int tw = blockIdx.x * kCombWaves + (threadIdx.x >> 6); tw < T; tw += gridDim.x * kCombWaves) {
+    const int t = __builtin_amdgcn_readfirstlane(tw);  // the wave's token: its routes and scalars load once
     Row row;
     topk_bwd_load(row, logits, indices, d_add, t, E, k, token_weight, aux_stats, d_aux);
     float ds[Row::KM];

@@ -478,7 +478,8 @@ __global__ __launch_bounds__(kRouterWaves * kWave) void router_topk_bwd_kernel(
     int bf16_terms) {
   using Row = TopkBwdRow<LPT, NPL, KT>;
   const int k = KT ? KT : k_rt;
-  const int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
+  int t = blockIdx.x * Tok<LPT>::kPerBlock + Tok<LPT>::slot();
+  if constexpr (LPT == kWave) t = __builtin_amdgcn_readfirstlane(t);  // one token per wave: scalar route loads
   if (t >= T) return;
   Row row;
   topk_bwd_load(row, logits, indices, d_add, t, E, k, token_weight, aux_stats, d_aux);
