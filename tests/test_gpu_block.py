@@ -244,6 +244,40 @@ def test_full_c2_forward_properties_and_sampled_tokens():
     close_bf16(out1.cpu()[sample], ref, "c2 sampled tokens")
 
 
+def test_full_c2_backward_sampled_tokens_against_the_oracle():
+    """The full C2 block's input gradient (the one-op block: the router's
+    top-k backward inside the combine backward, the router's dX added in the
+    permute backward) on 48 sampled tokens against the oracle run on those
+    tokens alone.  With no aux term every part of a token's input gradient
+    is the token's own: its k experts' backward and its router row's."""
+    w = WORKLOADS["c2"]
+    inp = make_block_inputs(w, seed=15, device=DEV, dtype=BF, weights_on_device_rng=True)
+    x = inp["x"].clone().requires_grad_()
+    rw, gu, dn = inp["router_weight"], inp["gate_up_proj"], inp["down_proj"]
+    out, logits, _, idx, _ = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob)
+    d_out = inp["d_out"]
+    torch.autograd.backward([out], [d_out])
+    torch.cuda.synchronize()
+    sample = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(1))[:48]
+    ref = O.block_forward_backward(x.detach().cpu()[sample], rw.cpu(), gu.cpu(), dn.cpu(), d_out.cpu()[sample],
+                                   top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=0.0)
+    routing_check(idx.cpu()[sample], ref["indices"], logits.detach().cpu()[sample])
+    close_bf16(out.detach().cpu()[sample], ref["out"], "c2 sampled out")
+    got = x.grad.cpu()[sample].float()
+    rel, _ = close_bf16(got, ref["dx"], "c2 sampled dx")
+    # The router's share of dx must be there: the oracle's input gradient
+    # with the routing weights held constant (experts only) is much further
+    # from the kernels' than the full one is.
+    xs = x.detach().cpu()[sample].float().requires_grad_()
+    _, ix = O.topk_softmax(O.router_logits(xs, rw.cpu()), w.top_k, w.norm_topk_prob)
+    sc = O.topk_softmax(O.router_logits(xs.detach(), rw.cpu()), w.top_k, w.norm_topk_prob)[0]
+    y = O.experts_grouped(xs, ix, sc, gu.cpu(), dn.cpu())
+    (y.float() * d_out.cpu()[sample].float()).sum().backward()
+    scale = ref["dx"].float().abs().max()
+    rel_experts_only = float((got - xs.grad).abs().max() / scale)
+    assert rel_experts_only > 4 * rel, (rel, rel_experts_only)
+
+
 def test_experts_concentrated_routing():
     """Every token routes to the same k experts: k groups of T rows (several
     evenly split m-tiles each) and E - k empty experts, forward and backward,
