@@ -244,33 +244,41 @@ def test_full_c2_forward_properties_and_sampled_tokens():
     close_bf16(out1.cpu()[sample], ref, "c2 sampled tokens")
 
 
-def test_full_c2_backward_sampled_tokens_against_the_oracle():
-    """The full C2 block's input gradient (the one-op block: the router's
+@pytest.mark.parametrize("name", ["c2", "c4", "c5"])
+def test_full_size_backward_sampled_tokens_against_the_oracle(name):
+    """The full block's input gradient (the one-op block: the router's
     top-k backward inside the combine backward, the router's dX added in the
     permute backward) on 48 sampled tokens against the oracle run on those
-    tokens alone.  With no aux term every part of a token's input gradient
-    is the token's own: its k experts' backward and its router row's."""
-    w = WORKLOADS["c2"]
+    tokens alone, at C2, C4 (its biased router) and C5 (H 4096).  With no
+    aux term every part of a token's input gradient is the token's own: its
+    k experts' backward and its router row's."""
+    w = WORKLOADS[name]
     inp = make_block_inputs(w, seed=15, device=DEV, dtype=BF, weights_on_device_rng=True)
     x = inp["x"].clone().requires_grad_()
     rw, gu, dn = inp["router_weight"], inp["gate_up_proj"], inp["down_proj"]
-    out, logits, _, idx, _ = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob)
+    bias = inp.get("logit_bias")
+    out, logits, _, idx, _ = ops.moe_block(x, rw, gu, dn, w.top_k, w.norm_topk_prob, None, bias)
     d_out = inp["d_out"]
     torch.autograd.backward([out], [d_out])
     torch.cuda.synchronize()
     sample = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(1))[:48]
+    bias_c = None if bias is None else bias.cpu()
     ref = O.block_forward_backward(x.detach().cpu()[sample], rw.cpu(), gu.cpu(), dn.cpu(), d_out.cpu()[sample],
-                                   top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=0.0)
+                                   top_k=w.top_k, norm_topk_prob=w.norm_topk_prob, aux_coef=0.0, logit_bias=bias_c)
     routing_check(idx.cpu()[sample], ref["indices"], logits.detach().cpu()[sample])
-    close_bf16(out.detach().cpu()[sample], ref["out"], "c2 sampled out")
+    close_bf16(out.detach().cpu()[sample], ref["out"], f"{name} sampled out")
     got = x.grad.cpu()[sample].float()
-    rel, _ = close_bf16(got, ref["dx"], "c2 sampled dx")
+    rel, _ = close_bf16(got, ref["dx"], f"{name} sampled dx")
     # The router's share of dx must be there: the oracle's input gradient
     # with the routing weights held constant (experts only) is much further
     # from the kernels' than the full one is.
     xs = x.detach().cpu()[sample].float().requires_grad_()
-    _, ix = O.topk_softmax(O.router_logits(xs, rw.cpu()), w.top_k, w.norm_topk_prob)
-    sc = O.topk_softmax(O.router_logits(xs.detach(), rw.cpu()), w.top_k, w.norm_topk_prob)[0]
+
+    def lg(t):
+        return O.router_logits(t, rw.cpu()) + (0.0 if bias_c is None else bias_c.float())
+
+    _, ix = O.topk_softmax(lg(xs), w.top_k, w.norm_topk_prob)
+    sc = O.topk_softmax(lg(xs.detach()), w.top_k, w.norm_topk_prob)[0]
     y = O.experts_grouped(xs, ix, sc, gu.cpu(), dn.cpu())
     (y.float() * d_out.cpu()[sample].float()).sum().backward()
     scale = ref["dx"].float().abs().max()
