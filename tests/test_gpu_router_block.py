@@ -363,7 +363,9 @@ COMBINE_ROUTER_CASES = [(4096, 2048, 128, 8, True, False, False, False, 0.0),
                         (512, 128, 200, 4, True, True, True, True, 0.0),
                         (300, 96, 32, 3, True, False, True, False, 0.1),
                         (64, 64, 1000, 16, True, True, False, True, 0.0),
-                        (33, 72, 8, 1, False, False, False, False, 0.0)]
+                        (33, 72, 8, 1, False, False, False, False, 0.0),
+                        # more tokens than the grid's waves: a wave takes several tokens
+                        (40000, 64, 64, 4, True, True, True, False, 0.02)]
 
 
 @pytest.mark.parametrize("T,H,E,k,norm,aux,d_logits,bf16,sentinel", COMBINE_ROUTER_CASES)
